@@ -1,0 +1,81 @@
+/*
+ * usagi_bsa.h — C ABI of the MI355X (gfx950) block-sparse causal attention forward.
+ *
+ * The reference exposes this path only as a Python submission module whose timed call is
+ *   block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens) -> (O, LSE)
+ * (kernels/v7_blockptr_warpspec.py:251-252), which flattens to [B*H, T, D] and launches one
+ * Triton program per (query block, b*h) (kernels/v7_blockptr_warpspec.py:155-191). The entry
+ * points below replace that launch (and the ctypes cuLaunchKernel hop of
+ * kernels/v1_baseline.py:93-128) with plain pointers and sizes: no torch types cross the
+ * boundary, and the library allocates no device memory.
+ *
+ * Conventions
+ *   - All tensor pointers are borrowed device pointers. Inputs are never written.
+ *   - q, k, v, out: contiguous [B, H, T, 128] of `dtype` (fp16, or bf16 with fp16 P·V).
+ *   - row_ptr: int32 [B, H, T/128 + 1]; values are offsets local to each (b, h) row of col_idx
+ *     (kernels/v7_blockptr_warpspec.py:77-80).
+ *   - col_idx: int32 [B, H, max_nnz]; row qb lists key blocks in
+ *     col_idx[b, h, row_ptr[qb] : row_ptr[qb+1]], ascending, with the diagonal (kb == qb) as the
+ *     LAST entry. The diagonal is processed implicitly and causally masked; entries before it are
+ *     processed unmasked (kernels/v7_blockptr_warpspec.py:83-136).
+ *   - seq_lens: int32 [B] or NULL (NULL: every sequence has length T). Query rows at or past
+ *     seq_len get O = 0 and LSE = -inf (kernels/v7_blockptr_warpspec.py:63-67, 138-148).
+ *   - lse: float32 [B, H, T], natural-log log-sum-exp of the scaled scores, or NULL to skip.
+ *   - stream: a hipStream_t (NULL = the default stream). The launch is asynchronous.
+ *   - Return: 0 on success; a negative USAGI_BSA_E* code for a rejected argument; a positive
+ *     hipError_t value when the HIP runtime reports an error. usagi_bsa_last_error() gives a
+ *     message for the calling thread's last failure.
+ */
+#ifndef USAGI_BSA_H
+#define USAGI_BSA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define USAGI_BSA_BLOCK 128
+#define USAGI_BSA_HEAD_DIM 128
+
+enum usagi_bsa_dtype {
+  USAGI_BSA_FP16 = 0, /* fp16 q/k/v/out (the build's contract) */
+  USAGI_BSA_BF16 = 1  /* bf16 q/k/v/out, fp16 P·V (kernels/v7_blockptr_warpspec.py:107) */
+};
+
+enum usagi_bsa_status {
+  USAGI_BSA_OK = 0,
+  USAGI_BSA_EINVAL = -1,   /* a null pointer or an out-of-range size */
+  USAGI_BSA_EDTYPE = -2,   /* unknown dtype code */
+  USAGI_BSA_EHEADDIM = -3, /* head_dim != 128 */
+  USAGI_BSA_ESEQ = -4,     /* T is not a positive multiple of 128 */
+  USAGI_BSA_ECSR = -5      /* malformed CSR (usagi_bsa_check_csr only) */
+};
+
+/* Forward pass. Replaces _run_csr + the _fwd_csr launch,
+ * kernels/v7_blockptr_warpspec.py:155-191 (same in kernels/v4_leaderboard_0740ms.py:143-179). */
+int usagi_bsa_fwd(const void* q, const void* k, const void* v,
+                  const int32_t* row_ptr, const int32_t* col_idx, const int32_t* seq_lens,
+                  void* out, float* lse,
+                  int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
+                  int32_t max_nnz, int32_t dtype, void* stream);
+
+/* Host-side CSR validator over HOST copies of row_ptr / col_idx. It checks the preconditions
+ * under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-111 equals
+ * block-mask ∧ causal attention: row_ptr[0] == 0, monotone, row_ptr[nqb] <= max_nnz, every row
+ * non-empty, strictly ascending, every entry in [0, qb], and the last entry == qb.
+ * Returns 0, or USAGI_BSA_ECSR with the first offending (b, h, qb) in usagi_bsa_last_error(). */
+int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
+                        int32_t batch, int32_t heads, int32_t num_q_blocks, int32_t max_nnz);
+
+/* Version string of this library, e.g. "usagi_bsa 0.1.0 gfx950". */
+const char* usagi_bsa_version(void);
+
+/* Message for the calling thread's most recent nonzero return ("" if none). */
+const char* usagi_bsa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* USAGI_BSA_H */

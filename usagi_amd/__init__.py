@@ -1,0 +1,15 @@
+"""usagi_amd — MI355X (gfx950) block-sparse causal attention forward.
+
+The reference's submission-module names are re-exported here:
+VARIANT_MANIFEST, setup, block_sparse_attn_fwd (kernels/v7_blockptr_warpspec.py:24, 201, 251).
+"""
+
+from .submission import (  # noqa: F401
+    BLOCK_SIZE,
+    HEAD_DIM,
+    VARIANT_MANIFEST,
+    block_sparse_attn_fwd,
+    setup,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,89 @@
+"""ctypes binding of libusagi_bsa.so (declarations in include/usagi_bsa.h).
+
+torch is imported first so that the library binds to the HIP runtime torch already loaded
+(one runtime per process). There is no fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load: shares torch's HIP runtime)
+
+from .build import LIB_PATH
+
+FP16 = 0
+BF16 = 1
+
+EXPORTED_SYMBOLS = (
+    "usagi_bsa_fwd",
+    "usagi_bsa_check_csr",
+    "usagi_bsa_version",
+    "usagi_bsa_last_error",
+)
+
+_lib = None
+
+
+class NativeError(RuntimeError):
+    """A nonzero status from the C ABI."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"usagi_bsa error {code}: {message}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"native library {LIB_PATH} is missing; build it with `python -m usagi_amd.build`"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    p = ctypes.c_void_p
+    i32 = ctypes.c_int32
+    lib.usagi_bsa_fwd.argtypes = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, p]
+    lib.usagi_bsa_fwd.restype = ctypes.c_int
+    lib.usagi_bsa_check_csr.argtypes = [p, p, i32, i32, i32, i32]
+    lib.usagi_bsa_check_csr.restype = ctypes.c_int
+    lib.usagi_bsa_version.argtypes = []
+    lib.usagi_bsa_version.restype = ctypes.c_char_p
+    lib.usagi_bsa_last_error.argtypes = []
+    lib.usagi_bsa_last_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().usagi_bsa_last_error().decode()
+
+
+def version() -> str:
+    return load().usagi_bsa_version().decode()
+
+
+def check(code: int) -> None:
+    if code != 0:
+        raise NativeError(code, last_error())
+
+
+def fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr, out_ptr, lse_ptr,
+        batch, heads, seq_len, head_dim, max_nnz, dtype, stream) -> None:
+    check(load().usagi_bsa_fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr,
+                               out_ptr, lse_ptr, batch, heads, seq_len, head_dim, max_nnz,
+                               dtype, stream))
+
+
+def check_csr_host(row_ptr, col_idx, batch: int, heads: int, nqb: int, max_nnz: int) -> None:
+    """Validate host (numpy int32, C-contiguous) CSR arrays through the C validator."""
+    import numpy as np
+
+    rp = np.ascontiguousarray(row_ptr, dtype=np.int32)
+    ci = np.ascontiguousarray(col_idx, dtype=np.int32)
+    code = load().usagi_bsa_check_csr(rp.ctypes.data, ci.ctypes.data if ci.size else None,
+                                      batch, heads, nqb, max_nnz)
+    if code != 0:
+        raise ValueError(f"malformed CSR: {last_error()}")

@@ -1,0 +1,62 @@
+"""Ahead-of-time build of the gfx950 HIP library (replaces the reference's Triton JIT warm-up,
+kernels/v7_blockptr_warpspec.py:195-247: nothing is compiled at run time here).
+
+    python -m usagi_amd.build            # builds usagi_amd/lib/libusagi_bsa.so
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+SRC = os.path.join(PKG_DIR, "csrc", "bsa_fwd.hip")
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libusagi_bsa.so")
+ARCH = "gfx950"
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc, PATH)")
+
+
+def hipcc_command(src: str = SRC, out: str = LIB_PATH, extra: list[str] | None = None) -> list[str]:
+    return [
+        hipcc_path(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # Packed FP32 VALU forms are kept out of the device code.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", INCLUDE_DIR,
+        *(extra or []),
+        src,
+        "-o", out,
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile the HIP source into an in-tree shared library; returns its path."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = hipcc_command(out=tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,450 @@
+// Block-sparse causal attention forward for MI355X (gfx950 / CDNA4).
+//
+// Semantics follow the reference Triton kernel _fwd_csr (kernels/v7_blockptr_warpspec.py:30-148,
+// same math as kernels/v4_leaderboard_0740ms.py:31-136): for each (b*h, query block qb) the
+// CSR row col_idx[row_ptr[qb] : row_ptr[qb+1]] lists key blocks, ascending, with the diagonal
+// last. Entries before the diagonal are attended unmasked (v7:83-108); the diagonal is taken
+// implicitly as kb = qb and causally masked (v7:111-136). Softmax is an online exp2 softmax
+// over fp32 scores scaled AFTER the dot product (v7:92, v7:96-100); P is rounded to fp16 before
+// P·V (v7:107). O = acc / l and LSE = m·ln2 + ln l (v7:138-148).
+//
+// MI355X design (not a translation of the Triton program):
+//   * One 256-thread workgroup (4 wave64s) per (b*h, qb); each wave owns 32 query rows.
+//   * Everything is computed transposed so that one lane owns one query row:
+//       S^T[key][q] = K · Q^T      (MFMA A = K rows from LDS, B = Q fragment in VGPRs)
+//       O^T[d][q]  += V^T · P^T    (MFMA A = V^T rows from LDS, B = P taken straight from the
+//                                   S^T accumulator registers, no LDS round trip)
+//     With v_mfma_f32_32x32x16_{f16,bf16}, lane l holds query (l % 32); the other 64 keys of
+//     that query sit in lane l ^ 32, so the row max is one v_permlane32_swap and the running
+//     row sum needs no cross-lane work until the epilogue.
+//   * K is staged in LDS row-major, V transposed (d-major) with the key order permuted inside
+//     each 16-key group so that the A operand of P·V is one 16-byte LDS read per lane.
+//     Rows are padded to 272 B to spread LDS banks. 68 KiB of LDS per workgroup.
+//   * The next K/V tile is fetched from HBM/L2 into VGPRs while the current one is consumed.
+//   * Workgroups are issued longest-row-first (query blocks in descending order, b*h fastest),
+//     which also keeps all query blocks of one (b, h) on one XCD when B*H is a multiple of 8.
+//   * The running max is only moved when it grows by more than 2^8, so the O rescale is
+//     skipped for almost every block while P stays <= 256 (exact in the normalised result).
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "usagi_bsa.h"
+
+namespace {
+
+constexpr int kBlk = USAGI_BSA_BLOCK;    // rows per query / key block
+constexpr int kHd = USAGI_BSA_HEAD_DIM;  // head dimension
+constexpr int kThreads = 256;            // 4 wave64s
+constexpr int kRow = kHd + 8;            // halfs per padded LDS row (272 B)
+constexpr float kTau = 8.0f;             // lazy-rescale threshold, log2 units
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct Args {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  const int32_t* row_ptr;
+  const int32_t* col_idx;
+  const int32_t* seq_lens;
+  int heads;
+  int T;
+  int nqb;
+  int bh_count;
+  int max_nnz;
+  float qk_scale;  // log2(e) / sqrt(128)
+};
+
+__device__ __forceinline__ float wave_pair_max(float x) {
+  // {x[l], x[l ^ 32]} in some order; max is symmetric.
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float wave_pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Two bf16 (one dword) -> two fp16 (one dword), round to nearest even.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+  const float lo = __uint_as_float(w << 16);
+  const float hi = __uint_as_float(w & 0xffff0000u);
+  const _Float16 a = (_Float16)lo;
+  const _Float16 b = (_Float16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ uint16_t to_out_bits(float x, bool bf16) {
+  if (bf16) return __builtin_bit_cast(uint16_t, (__bf16)x);
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ floatx16 mfma_qk(u32x4 a, u32x4 b, floatx16 c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ floatx16 mfma_pv(u32x4 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a), b, c, 0, 0, 0);
+}
+
+template <bool kBf16>
+__global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBlk * kRow];   // K[key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kHd * kRow];   // V^T[d][key'] (fp16)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 31;
+  const int lh = lane >> 5;
+
+  // Longest-row-first issue order: descending query block, b*h fastest.
+  const int item = blockIdx.x;
+  const int qslot = item / a.bh_count;
+  const int qb = a.nqb - 1 - qslot;
+  const int bh = item - qslot * a.bh_count;
+  const int seq_len = a.seq_lens ? a.seq_lens[bh / a.heads] : a.T;
+  const int q0 = qb * kBlk;
+  const size_t base = (size_t)bh * a.T * kHd;
+  uint16_t* out_blk = a.o + base + (size_t)q0 * kHd;
+
+  if (q0 >= seq_len) {
+    // Whole query block past the sequence: O = 0, LSE = -inf (v7:63-67).
+#pragma unroll
+    for (int i = 0; i < (kBlk * kHd) / (8 * kThreads); ++i) {
+      *(u32x4*)(out_blk + (size_t)(i * kThreads + tid) * 8) = u32x4{0, 0, 0, 0};
+    }
+    if (a.lse && tid < kBlk) a.lse[(size_t)bh * a.T + q0 + tid] = -INFINITY;
+    return;
+  }
+
+  const int q_local = wave * 32 + li;
+  const int qrow = q0 + q_local;
+  const bool qvalid = qrow < seq_len;
+  const bool full_q = q0 + kBlk <= seq_len;  // uniform: no query row of the block is masked
+
+  // Q^T fragment (MFMA B operand): lane holds Q[qrow][16s + 8lh .. +8] for s = 0..7.
+  u32x4 qf[8];
+  {
+    const uint16_t* qp = a.q + base + (size_t)qrow * kHd + 8 * lh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const u32x4*)(qp + 16 * s);
+  }
+
+  // CSR row (offsets local to this b*h, v7:77-80). Clamped so a malformed row cannot index
+  // outside col_idx or outside K/V; the host validator reports such rows as errors.
+  const int32_t* rp = a.row_ptr + (size_t)bh * (a.nqb + 1) + qb;
+  int rs = rp[0];
+  int re = rp[1];
+  rs = min(max(rs, 0), a.max_nnz);
+  re = min(max(re, rs), a.max_nnz);
+  const int n_off = max(re - rs - 1, 0);  // off-diagonal entries; the last entry is the diagonal
+  const int32_t* cols = a.col_idx + (size_t)bh * a.max_nnz + rs;
+  const int nqb_m1 = a.nqb - 1;
+  auto key_block = [&](int j) -> int {
+    if (j >= n_off) return qb;
+    const int kb = cols[j];
+    return min(max(kb, 0), nqb_m1);
+  };
+
+  // Tile staging. K: chunk c = i*256 + tid -> row c/16, 8 halfs at (c%16)*8.
+  // V: thread owns 8 keys x 8 d: d chunk dc, key group kg holding keys
+  //    16*(kg/2) + 4*(kg%2) + {0,1,2,3} and +8 + {0,1,2,3}, written transposed so that
+  //    V^T row d, positions 8kg .. 8kg+7 hold exactly those keys in that order.
+  const int v_dc = (tid >> 2) & 15;
+  const int v_kg = (tid & 3) + 4 * wave;
+  const int v_key0 = 16 * (v_kg >> 1) + 4 * (v_kg & 1);
+  u32x4 kst[8];
+  u32x4 vst[8];
+
+  auto load_tile = [&](int kb) {
+    const uint16_t* kp = a.k + base + (size_t)kb * kBlk * kHd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = i * kThreads + tid;
+      kst[i] = *(const u32x4*)(kp + (c >> 4) * kHd + (c & 15) * 8);
+    }
+    const uint16_t* vp = a.v + base + (size_t)kb * kBlk * kHd + v_dc * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = v_key0 + (e & 3) + 8 * (e >> 2);
+      vst[e] = *(const u32x4*)(vp + key * kHd);
+    }
+  };
+
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = i * kThreads + tid;
+      *(u32x4*)(k_lds + (c >> 4) * kRow + (c & 15) * 8) = kst[i];
+    }
+    if constexpr (kBf16) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vst[e][w] = bf16x2_to_f16x2(vst[e][w]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w[j] = __builtin_amdgcn_perm(vst[2 * j + 1][d >> 1], vst[2 * j][d >> 1], sel);
+      }
+      *(u32x4*)(vt_lds + (v_dc * 8 + d) * kRow + v_kg * 8) = w;
+    }
+  };
+
+  floatx16 o_acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[u][r] = 0.0f;
+  }
+  float m_used = -1e30f;  // running max in log2 units (v7:73)
+  float l_part = 0.0f;    // this lane's half of the running row sum
+  const float scale = a.qk_scale;
+
+  const int nblk = n_off + 1;
+  load_tile(key_block(0));
+
+  for (int j = 0; j < nblk; ++j) {
+    if (j) __syncthreads();  // every wave is done reading the previous tile
+    store_tile();
+    __syncthreads();
+    const bool diag = (j == n_off);
+    if (j + 1 < nblk) load_tile(key_block(j + 1));
+
+    // S^T = K · Q^T: st[t][r] = S[q_local][key], key = 32t + 8(r/4) + 4lh + r%4.
+    floatx16 st[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[t][r] = 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4 ka = *(const u32x4*)(k_lds + (32 * t + li) * kRow + 16 * s + 8 * lh);
+        st[t] = mfma_qk<kBf16>(ka, qf[s], st[t]);
+      }
+    }
+
+    // Masks: causal on the diagonal (v7:119-122), invalid query rows everywhere (v7:94).
+    if (diag) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * t + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (key > q_local || !qvalid) st[t][r] = -INFINITY;
+        }
+      }
+    } else if (!full_q && !qvalid) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
+      }
+    }
+
+    // Online softmax in log2 units.
+    float mx = st[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
+    }
+    mx = wave_pair_max(mx);
+    const float m_cand = fmaxf(m_used, mx * scale);
+    const bool grow = m_cand > m_used + kTau;
+    if (__any(grow)) {
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - m_cand) : 1.0f;
+      m_used = grow ? m_cand : m_used;
+      l_part *= alpha;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[u][r] *= alpha;
+      }
+    }
+    const float neg_m = -m_used;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[t][r], scale, neg_m));
+        st[t][r] = p;
+        psum += p;
+      }
+    }
+    l_part += psum;
+
+    // P^T fragments (MFMA B operand of P·V): k-step s covers keys 16s + 8(e/4) + 4lh + e%4.
+    half8 pb[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[s][e] = (_Float16)st[s >> 1][8 * (s & 1) + e];
+    }
+
+    // O^T += V^T · P^T: o_acc[u][r] = O[q_local][d], d = 32u + 8(r/4) + 4lh + r%4.
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x4 va = *(const u32x4*)(vt_lds + (32 * u + li) * kRow + 16 * s + 8 * lh);
+        o_acc[u] = mfma_pv(va, pb[s], o_acc[u]);
+      }
+    }
+  }
+
+  // Epilogue (v7:138-148).
+  const float l_tot = wave_pair_sum(l_part);
+  float inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;
+  if (!qvalid) inv = 0.0f;
+  uint16_t* orow = a.o + base + (size_t)qrow * kHd + 4 * lh;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w[0] = (uint32_t)to_out_bits(o_acc[u][4 * g + 0] * inv, kBf16) |
+             ((uint32_t)to_out_bits(o_acc[u][4 * g + 1] * inv, kBf16) << 16);
+      w[1] = (uint32_t)to_out_bits(o_acc[u][4 * g + 2] * inv, kBf16) |
+             ((uint32_t)to_out_bits(o_acc[u][4 * g + 3] * inv, kBf16) << 16);
+      *(u32x2*)(orow + 32 * u + 8 * g) = w;
+    }
+  }
+  if (a.lse && lh == 0) {
+    const float lse = (qvalid && l_tot > 0.0f) ? (m_used + log2f(l_tot)) * kLn2 : -INFINITY;
+    a.lse[(size_t)bh * a.T + qrow] = lse;
+  }
+}
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+}  // namespace
+
+extern "C" const char* usagi_bsa_version(void) { return "usagi_bsa 0.1.0 gfx950"; }
+
+extern "C" const char* usagi_bsa_last_error(void) { return g_err; }
+
+extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
+                             const int32_t* row_ptr, const int32_t* col_idx,
+                             const int32_t* seq_lens, void* out, float* lse, int32_t batch,
+                             int32_t heads, int32_t seq_len, int32_t head_dim, int32_t max_nnz,
+                             int32_t dtype, void* stream) {
+  g_err[0] = '\0';
+  if (!q || !k || !v || !row_ptr || !out) return fail(USAGI_BSA_EINVAL, "null tensor pointer");
+  if (dtype != USAGI_BSA_FP16 && dtype != USAGI_BSA_BF16)
+    return fail(USAGI_BSA_EDTYPE, "unknown dtype code %d", (int)dtype);
+  if (head_dim != kHd) return fail(USAGI_BSA_EHEADDIM, "head_dim must be %d, got %d", kHd, (int)head_dim);
+  if (seq_len <= 0 || seq_len % kBlk != 0)
+    return fail(USAGI_BSA_ESEQ, "T must be a positive multiple of %d, got %d", kBlk, (int)seq_len);
+  if (batch <= 0 || heads <= 0) return fail(USAGI_BSA_EINVAL, "batch and heads must be positive");
+  if (max_nnz < 0 || (max_nnz > 0 && !col_idx))
+    return fail(USAGI_BSA_EINVAL, "max_nnz must be >= 0 and col_idx non-null when max_nnz > 0");
+  const long long bh = (long long)batch * heads;
+  const long long nqb = seq_len / kBlk;
+  if (bh * nqb > 0x7fffffffLL || bh > 0x7fffffffLL / ((long long)seq_len * kHd) ||
+      bh * (nqb + 1) > 0x7fffffffLL || bh * (long long)max_nnz > 0x7fffffffLL * 4LL)
+    return fail(USAGI_BSA_EINVAL, "problem too large");
+
+  Args a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.row_ptr = row_ptr;
+  a.col_idx = col_idx;
+  a.seq_lens = seq_lens;
+  a.heads = heads;
+  a.T = seq_len;
+  a.nqb = (int)nqb;
+  a.bh_count = (int)bh;
+  a.max_nnz = max_nnz;
+  a.qk_scale = (float)(1.4426950408889634 / sqrt((double)kHd));
+
+  const dim3 grid((unsigned)(bh * nqb));
+  const dim3 block(kThreads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == USAGI_BSA_BF16) {
+    hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(bsa_fwd_kernel<false>, grid, block, 0, s, a);
+  }
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return USAGI_BSA_OK;
+}
+
+extern "C" int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx, int32_t batch,
+                                   int32_t heads, int32_t num_q_blocks, int32_t max_nnz) {
+  g_err[0] = '\0';
+  if (!row_ptr || batch <= 0 || heads <= 0 || num_q_blocks <= 0 || max_nnz < 0 ||
+      (max_nnz > 0 && !col_idx))
+    return fail(USAGI_BSA_EINVAL, "bad arguments");
+  const int64_t bh_count = (int64_t)batch * heads;
+  for (int64_t bh = 0; bh < bh_count; ++bh) {
+    const int32_t* rp = row_ptr + bh * (num_q_blocks + 1);
+    const int32_t* ci = col_idx ? col_idx + bh * (int64_t)max_nnz : nullptr;
+    const int b = (int)(bh / heads), h = (int)(bh % heads);
+    if (rp[0] != 0) return fail(USAGI_BSA_ECSR, "(b=%d,h=%d): row_ptr[0]=%d, expected 0", b, h, rp[0]);
+    if (rp[num_q_blocks] > max_nnz)
+      return fail(USAGI_BSA_ECSR, "(b=%d,h=%d): row_ptr[%d]=%d exceeds max_nnz=%d", b, h,
+                  num_q_blocks, rp[num_q_blocks], max_nnz);
+    for (int qb = 0; qb < num_q_blocks; ++qb) {
+      const int rs = rp[qb], re = rp[qb + 1];
+      if (re <= rs)
+        return fail(USAGI_BSA_ECSR, "(b=%d,h=%d,qb=%d): empty or decreasing row (%d..%d)", b, h,
+                    qb, rs, re);
+      for (int j = rs; j < re; ++j) {
+        const int kb = ci[j];
+        if (kb < 0 || kb > qb)
+          return fail(USAGI_BSA_ECSR, "(b=%d,h=%d,qb=%d): key block %d outside [0, %d]", b, h,
+                      qb, kb, qb);
+        if (j > rs && kb <= ci[j - 1])
+          return fail(USAGI_BSA_ECSR, "(b=%d,h=%d,qb=%d): col_idx not strictly ascending", b, h, qb);
+      }
+      if (ci[re - 1] != qb)
+        return fail(USAGI_BSA_ECSR, "(b=%d,h=%d,qb=%d): last entry %d is not the diagonal", b, h,
+                    qb, ci[re - 1]);
+    }
+  }
+  return USAGI_BSA_OK;
+}

@@ -1,0 +1,136 @@
+"""Submission-module entry points, same names and contract as the reference
+(kernels/v7_blockptr_warpspec.py:15-24, 201-252):
+
+    VARIANT_MANIFEST
+    setup(suite_specs, device, variants)
+    block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens) -> (O, LSE)
+
+Differences from the reference, all deliberate:
+  * fp16 q/k/v/O is the primary dtype; bf16 is also accepted (O in bf16, P·V in fp16 as in
+    kernels/v7_blockptr_warpspec.py:107).
+  * The launch goes through the C ABI of libusagi_bsa.so (compiled ahead of time for gfx950)
+    instead of a Triton JIT launch; there is no metadata cache keyed on data_ptr()
+    (kernels/v7_blockptr_warpspec.py:167-176): int32 contiguous CSR tensors are used in place,
+    anything else is converted on every call.
+  * `setup` raises instead of silently returning None when no ROCm device is usable
+    (kernels/v7_blockptr_warpspec.py:202-203), because there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+from . import _native
+
+BLOCK_SIZE = 128
+HEAD_DIM = 128
+_SCORE_SCALE = 1.0 / math.sqrt(HEAD_DIM)
+_LOG2E = math.log2(math.e)
+_QK_SCALE = _SCORE_SCALE * _LOG2E
+_LN2 = math.log(2.0)
+
+VARIANT_MANIFEST = [{"name": "default"}]
+
+# USAGI_BSA_VALIDATE=1 copies the CSR to the host on every call and checks it (synchronises).
+VALIDATE_CSR = os.environ.get("USAGI_BSA_VALIDATE", "0") not in ("", "0")
+
+_DTYPE_CODES = {torch.float16: _native.FP16, torch.bfloat16: _native.BF16}
+
+
+def _as_int32_device(t: torch.Tensor, device: torch.device, shape: tuple) -> torch.Tensor:
+    t = t.reshape(shape)
+    if t.device != device or t.dtype != torch.int32 or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.int32).contiguous()
+    return t
+
+
+def _check_inputs(q, k, v):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
+        if t.dtype not in _DTYPE_CODES:
+            raise TypeError(f"{name} must be float16 or bfloat16, got {t.dtype}")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be [B, H, T, D], got shape {tuple(t.shape)}")
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"q/k/v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q/k/v dtypes differ")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q/k/v are on different devices")
+    B, H, T, D = q.shape
+    if D != HEAD_DIM:
+        raise ValueError(f"head dim must be {HEAD_DIM}, got {D}")
+    if T <= 0 or T % BLOCK_SIZE:
+        raise ValueError(f"T must be a positive multiple of {BLOCK_SIZE}, got {T}")
+    return B, H, T, D
+
+
+def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
+    """Block-sparse causal attention forward.
+
+    q, k, v: [B, H, T, 128] fp16 (or bf16) on the GPU.
+    row_ptr: [B, H, T/128 + 1] integer, offsets local to each (b, h) row of col_idx.
+    col_idx: [B, H, max_nnz] integer; each row ascending with the diagonal last.
+    seq_lens: [B] integer (or None = all T).
+    Returns (O [B, H, T, 128] in q.dtype, LSE [B, H, T] float32), as
+    kernels/v7_blockptr_warpspec.py:191.
+    """
+    B, H, T, D = _check_inputs(q, k, v)
+    dev = q.device
+    nqb = T // BLOCK_SIZE
+    q = q.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    rp = _as_int32_device(row_ptr, dev, (B, H, nqb + 1))
+    max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
+    ci = _as_int32_device(col_idx, dev, (B, H, max_nnz))
+    sl = None
+    if seq_lens is not None:
+        sl = _as_int32_device(torch.as_tensor(seq_lens), dev, (B,))
+
+    if VALIDATE_CSR:
+        _native.check_csr_host(rp.cpu().numpy(), ci.cpu().numpy(), B, H, nqb, max_nnz)
+
+    out = torch.empty((B, H, T, D), device=dev, dtype=q.dtype)
+    lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), rp.data_ptr(),
+                    ci.data_ptr() if max_nnz else None, sl.data_ptr() if sl is not None else None,
+                    out.data_ptr(), lse.data_ptr(), B, H, T, D, max_nnz,
+                    _DTYPE_CODES[q.dtype], stream)
+    return out, lse
+
+
+def setup(suite_specs, device, variants):
+    """Load the ahead-of-time library and run one tiny launch per distinct T.
+
+    Mirrors kernels/v7_blockptr_warpspec.py:201-247 (a diagonal-only CSR per spec, then a
+    synchronise). Specs only need a `t_max` attribute.
+    """
+    _native.load()
+    if not suite_specs:
+        return None
+    dev = torch.device(device)
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        raise RuntimeError(f"usagi_amd needs a ROCm GPU device, got {device!r}")
+    seen = set()
+    for spec in suite_specs:
+        T = int(spec.t_max)
+        if T in seen:
+            continue
+        seen.add(T)
+        nqb = T // BLOCK_SIZE
+        x = torch.zeros((1, 1, T, HEAD_DIM), device=dev, dtype=torch.float16)
+        rp = torch.arange(nqb + 1, device=dev, dtype=torch.int32).view(1, 1, nqb + 1)
+        ci = torch.arange(nqb, device=dev, dtype=torch.int32).view(1, 1, nqb)
+        sl = torch.tensor([T], device=dev, dtype=torch.int32)
+        block_sparse_attn_fwd(x, x, x, rp, ci, sl)
+    torch.cuda.synchronize(dev)
+    return None
