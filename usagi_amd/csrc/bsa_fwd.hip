@@ -32,6 +32,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "usagi_bsa.h"
@@ -46,6 +47,7 @@ constexpr float kTau = 8.0f;             // lazy-rescale threshold, log2 units
 constexpr float kLn2 = 0.6931471805599453f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -347,7 +349,314 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// fp16 kernel: K and V tiles go HBM -> LDS by direct DMA (global_load_lds_dwordx4), so no VGPRs
+// stage them; V is read transposed out of LDS with ds_read_b64_tr_b16. That keeps the wave at
+// <= 256 registers, so two workgroups share each CU (2 waves per SIMD): while one workgroup
+// waits at a barrier or runs softmax VALU, the other keeps the matrix core busy.
+//
+// LDS tiles are 128 rows x 256 B, unpadded, with 16-byte chunks XOR-swizzled inside each row
+// (K: chunk ^ (row % 16), V: chunk ^ 4 * (row % 4)) so that both the DMA writes (1 KiB
+// lane-contiguous per wave instruction) and the MFMA operand reads spread over all banks.
+//
+// Per key block j (three barriers, tiles single-buffered per workgroup):
+//   wait K(j)  | barrier | S^T = K·Q^T     | wait V(j) | barrier | DMA K(j+1)
+//   softmax    | O^T += V^T·P^T           | barrier   | DMA V(j+1)
+// ---------------------------------------------------------------------------------------------
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_cvoid;
+
+// One 16-byte-per-lane DMA: global (uniform base + per-lane byte offset) -> LDS at the uniform
+// byte address lds_addr + 16 * lane. Issued as inline asm so that the compiler's wait-count pass
+// does not treat it as aliasing every later LDS read; the kernel waits for it explicitly
+// (s_waitcnt vmcnt + s_barrier) before any wave reads the tile.
+template <int kImm>
+__device__ __forceinline__ void dma_16b(const void* gbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3 offset:%4\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff), "s"(gbase), "i"(kImm)
+      : "memory");
+}
+
+// 8 DMAs of one wave's 8 KiB share of a tile: instruction i moves row group i (1 KiB). The
+// instruction's immediate offset moves both the global and the LDS address, so 1024 (i % 4) goes
+// there and i >= 4 use global and LDS bases 4096 bytes further on.
+__device__ __forceinline__ void dma_tile8(const char* src, const uint32_t off[4], uint32_t lds) {
+  const char* src_hi = src + 4096;
+  const uint32_t lds_hi = lds + 4096;
+  dma_16b<0>(src, off[0], lds);
+  dma_16b<1024>(src, off[1], lds);
+  dma_16b<2048>(src, off[2], lds);
+  dma_16b<3072>(src, off[3], lds);
+  dma_16b<0>(src_hi, off[0], lds_hi);
+  dma_16b<1024>(src_hi, off[1], lds_hi);
+  dma_16b<2048>(src_hi, off[2], lds_hi);
+  dma_16b<3072>(src_hi, off[3], lds_hi);
+}
+
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+#define USAGI_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+#define USAGI_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bsa_fwd_dma_kernel(Args a) {
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kBlk * kHd];  // K[key][d], swizzled
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kBlk * kHd];  // V[key][d], swizzled
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 31;
+  const int lh = lane >> 5;
+
+  const int item = blockIdx.x;
+  const int qslot = item / a.bh_count;
+  const int qb = a.nqb - 1 - qslot;
+  const int bh = item - qslot * a.bh_count;
+  const int seq_len = a.seq_lens ? a.seq_lens[bh / a.heads] : a.T;
+  const int q0 = qb * kBlk;
+  const size_t base = (size_t)bh * a.T * kHd;
+
+  if (q0 >= seq_len) {
+    uint16_t* out_blk = a.o + base + (size_t)q0 * kHd;
+#pragma unroll
+    for (int i = 0; i < (kBlk * kHd) / (8 * kThreads); ++i) {
+      *(u32x4*)(out_blk + (size_t)(i * kThreads + tid) * 8) = u32x4{0, 0, 0, 0};
+    }
+    if (a.lse && tid < kBlk) a.lse[(size_t)bh * a.T + q0 + tid] = -INFINITY;
+    return;
+  }
+
+  const int q_local = wave * 32 + li;
+  const int qrow = q0 + q_local;
+  const bool qvalid = qrow < seq_len;
+  const bool full_q = q0 + kBlk <= seq_len;
+
+  u32x4 qf[8];
+  {
+    const uint16_t* qp = a.q + base + (size_t)qrow * kHd + 8 * lh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = *(const u32x4*)(qp + 16 * s);
+  }
+
+  const int32_t* rp = a.row_ptr + (size_t)bh * (a.nqb + 1) + qb;
+  int rs = rp[0];
+  int re = rp[1];
+  rs = min(max(rs, 0), a.max_nnz);
+  re = min(max(re, rs), a.max_nnz);
+  const int n_off = max(re - rs - 1, 0);
+  const int32_t* cols = a.col_idx + (size_t)bh * a.max_nnz + rs;
+  const int nqb_m1 = a.nqb - 1;
+  // Column indices are held 64 at a time in one VGPR (lane i: entry 64c + i) and picked with
+  // v_readlane, so no vector load sits inside the loop behind the in-flight tile DMAs. Rows
+  // longer than 64 blocks reload the next chunk when they reach it.
+  int col_chunk = 0;
+  int colv = lane < n_off ? cols[lane] : 0;
+  auto key_block = [&](int j) -> int {
+    if (j >= n_off) return qb;
+    const int c = j >> 6;
+    if (c != col_chunk) {
+      col_chunk = c;
+      const int e = c * 64 + lane;
+      colv = e < n_off ? cols[e] : 0;
+    }
+    const int kb = __builtin_amdgcn_readlane(colv, j & 63);
+    return min(max(kb, 0), nqb_m1);
+  };
+
+  // DMA: wave w, instruction i writes row group 8w + i (rows 32w + 4i + L/16, 1 KiB per wave
+  // instruction). Lane L covers physical chunk L%16 = logical chunk (L%16) ^ swz(row). The
+  // per-lane byte offsets repeat for every tile, so only the uniform tile base changes.
+  const int dma_r = lane >> 4;
+  const int dma_pc = lane & 15;
+  // Row 32w + 4i + L/16 has (row % 16) = 4(i % 4) + L/16 and (row % 4) = L/16.
+  uint32_t k_off[4];
+  uint32_t v_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * i + dma_r)));
+    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * dma_r)));
+  }
+  const uint32_t k_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(k_lds) + wave * 8192);
+  const uint32_t v_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(v_lds) + wave * 8192);
+  auto issue_k = [&](int kb) {
+    dma_tile8((const char*)(a.k + base) + (size_t)kb * (kBlk * kHd * 2), k_off, k_dst);
+  };
+  auto issue_v = [&](int kb) {
+    dma_tile8((const char*)(a.v + base) + (size_t)kb * (kBlk * kHd * 2), v_off, v_dst);
+  };
+
+  // K operand (MFMA A, 32 keys x 16 d): lane reads row 32t + li, logical chunk 2s + lh.
+  const char* k_rd = (const char*)k_lds + li * 256;
+  const int k_x = lh ^ (li & 15);
+  // V^T operand via transpose reads: source lane l supplies row key0 + (l%16)/4 and the
+  // 8 bytes at d = 32u + 16((l/16)%2) + 4(l%4); key0 = 16s + 8r + 4lh.
+  const int tq = (lane & 15) >> 2;
+  const int t_x = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const char* v_rd = (const char*)v_lds + (4 * lh + tq) * 256 + 8 * (lane & 1);
+
+  floatx16 o_acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[u][r] = 0.0f;
+  }
+  float m_used = -1e30f;
+  float l_part = 0.0f;
+  const float scale = a.qk_scale;
+
+  const int nblk = n_off + 1;
+  issue_k(key_block(0));
+  issue_v(key_block(0));
+  // vmcnt(0): Q (and the first tiles) have landed. Issued as a real s_waitcnt so the compiler
+  // knows no load of its own is outstanding inside the loop.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  for (int j = 0; j < nblk; ++j) {
+    const bool diag = (j == n_off);
+    USAGI_WAIT_VM(8);  // this wave's K(j) DMA has landed (V(j) may still be in flight)
+    USAGI_BARRIER();
+
+    floatx16 st[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[t][r] = 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int off = 16 * ((2 * s) ^ k_x);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4 ka = *(const u32x4*)(k_rd + t * 8192 + off);
+        st[t] = mfma_qk<false>(ka, qf[s], st[t]);
+      }
+    }
+
+    USAGI_WAIT_VM(0);  // V(j) has landed
+    USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
+    if (j + 1 < nblk) issue_k(key_block(j + 1));
+
+    if (diag) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * t + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (key > q_local || !qvalid) st[t][r] = -INFINITY;
+        }
+      }
+    } else if (!full_q && !qvalid) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
+      }
+    }
+
+    float mx = st[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
+    }
+    mx = wave_pair_max(mx);
+    const float m_cand = fmaxf(m_used, mx * scale);
+    const bool grow = m_cand > m_used + kTau;
+    if (__any(grow)) {
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - m_cand) : 1.0f;
+      m_used = grow ? m_cand : m_used;
+      l_part *= alpha;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[u][r] *= alpha;
+      }
+    }
+    const float neg_m = -m_used;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[t][r], scale, neg_m));
+        st[t][r] = p;
+        psum += p;
+      }
+    }
+    l_part += psum;
+
+#pragma unroll
+    for (int hk = 0; hk < 2; ++hk) {  // keys 64hk .. 64hk+63
+      half8 pb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[s][e] = (_Float16)st[2 * hk + (s >> 1)][8 * (s & 1) + e];
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const char* vb = v_rd + 16 * (4 * (u ^ tq) + t_x) + (4 * hk + s) * 4096;
+          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
+          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
+          const half8 va = __builtin_shufflevector(__builtin_bit_cast(half4, lo),
+                                                   __builtin_bit_cast(half4, hi), 0, 1, 2, 3, 4, 5, 6, 7);
+          o_acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s], o_acc[u], 0, 0, 0);
+        }
+      }
+    }
+
+    USAGI_BARRIER();  // every wave is done reading V(j)
+    if (j + 1 < nblk) issue_v(key_block(j + 1));
+  }
+
+  const float l_tot = wave_pair_sum(l_part);
+  float inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;
+  if (!qvalid) inv = 0.0f;
+  uint16_t* orow = a.o + base + (size_t)qrow * kHd + 4 * lh;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w[0] = (uint32_t)to_out_bits(o_acc[u][4 * g + 0] * inv, false) |
+             ((uint32_t)to_out_bits(o_acc[u][4 * g + 1] * inv, false) << 16);
+      w[1] = (uint32_t)to_out_bits(o_acc[u][4 * g + 2] * inv, false) |
+             ((uint32_t)to_out_bits(o_acc[u][4 * g + 3] * inv, false) << 16);
+      *(u32x2*)(orow + 32 * u + 8 * g) = w;
+    }
+  }
+  if (a.lse && lh == 0) {
+    const float lse = (qvalid && l_tot > 0.0f) ? (m_used + log2f(l_tot)) * kLn2 : -INFINITY;
+    a.lse[(size_t)bh * a.T + qrow] = lse;
+  }
+}
+
 thread_local char g_err[512] = "";
+
+// USAGI_BSA_FP16_KERNEL=staged selects the register-staged kernel for fp16 as well (A/B runs).
+bool staged_fp16() {
+  static const bool v = [] {
+    const char* e = getenv("USAGI_BSA_FP16_KERNEL");
+    return e && strcmp(e, "staged") == 0;
+  }();
+  return v;
+}
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -405,8 +714,10 @@ extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == USAGI_BSA_BF16) {
     hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
-  } else {
+  } else if (staged_fp16()) {
     hipLaunchKernelGGL(bsa_fwd_kernel<false>, grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(bsa_fwd_dma_kernel, grid, block, 0, s, a);
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
