@@ -8,7 +8,14 @@
 // over fp32 scores scaled AFTER the dot product (v7:92, v7:96-100); P is rounded to fp16 before
 // P·V (v7:107). O = acc / l and LSE = m·ln2 + ln l (v7:138-148).
 //
-// MI355X design (not a translation of the Triton program):
+// Two kernels share that structure:
+//   bsa_fwd_dma_kernel      fp16 (the default): K/V tiles DMA'd HBM -> LDS, V read transposed
+//                           out of LDS, two workgroups per CU (see the comment at the kernel).
+//   bsa_fwd_kernel<bf16>    register-staged K/V (global -> VGPR -> LDS, V transposed and
+//                           converted to fp16 on the way in); used for bf16 inputs and, with
+//                           USAGI_BSA_FP16_KERNEL=staged, for fp16 A/B runs.
+//
+// Common MI355X design points (not a translation of the Triton program):
 //   * One 256-thread workgroup (4 wave64s) per (b*h, qb); each wave owns 32 query rows.
 //   * Everything is computed transposed so that one lane owns one query row:
 //       S^T[key][q] = K · Q^T      (MFMA A = K rows from LDS, B = Q fragment in VGPRs)
@@ -17,10 +24,6 @@
 //     With v_mfma_f32_32x32x16_{f16,bf16}, lane l holds query (l % 32); the other 64 keys of
 //     that query sit in lane l ^ 32, so the row max is one v_permlane32_swap and the running
 //     row sum needs no cross-lane work until the epilogue.
-//   * K is staged in LDS row-major, V transposed (d-major) with the key order permuted inside
-//     each 16-key group so that the A operand of P·V is one 16-byte LDS read per lane.
-//     Rows are padded to 272 B to spread LDS banks. 68 KiB of LDS per workgroup.
-//   * The next K/V tile is fetched from HBM/L2 into VGPRs while the current one is consumed.
 //   * Workgroups are issued longest-row-first (query blocks in descending order, b*h fastest),
 //     which also keeps all query blocks of one (b, h) on one XCD when B*H is a multiple of 8.
 //   * The running max is only moved when it grows by more than 2^8, so the O rescale is
@@ -35,6 +38,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "usagi_bsa.h"
 
 namespace {
@@ -48,6 +53,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -360,9 +366,12 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
 // (K: chunk ^ (row % 16), V: chunk ^ 4 * (row % 4)) so that both the DMA writes (1 KiB
 // lane-contiguous per wave instruction) and the MFMA operand reads spread over all banks.
 //
-// Per key block j (three barriers, tiles single-buffered per workgroup):
-//   wait K(j)  | barrier | S^T = K·Q^T     | wait V(j) | barrier | DMA K(j+1)
-//   softmax    | O^T += V^T·P^T           | barrier   | DMA V(j+1)
+// Per key block j (three barriers, tiles single-buffered per workgroup, 64 KiB of LDS):
+//   wait K(j) | barrier | S^T = K·Q^T, DMA of V(j) spread between the MFMAs | max, rescale
+//   wait V(j) | barrier | exp2 / fp16 P, O^T += V^T·P^T, DMA of K(j+1) spread between the MFMAs
+//   barrier
+// A 16-byte-per-lane LDS DMA holds the issuing wave for tens of cycles, so the eight 1 KiB
+// pieces of a wave's share are interleaved with MFMAs instead of being issued back to back.
 // ---------------------------------------------------------------------------------------------
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -376,14 +385,13 @@ typedef __attribute__((address_space(1))) const void global_cvoid;
 // (s_waitcnt vmcnt + s_barrier) before any wave reads the tile.
 template <int kImm>
 __device__ __forceinline__ void dma_16b(const void* gbase, uint32_t voff, uint32_t lds_addr) {
-  uint32_t saved;
+  // M0 holds the LDS destination. Nothing else in these kernels uses M0 (gfx950 LDS
+  // instructions do not read it), so it is not saved.
   asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, %3 offset:%4\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
+      "global_load_lds_dwordx4 %1, %2 offset:%3"
+      :
       : "s"(lds_addr), "v"(voff), "s"(gbase), "i"(kImm)
       : "memory");
 }
@@ -495,9 +503,21 @@ void bsa_fwd_dma_kernel(Args a) {
   auto issue_k = [&](int kb) {
     dma_tile8((const char*)(a.k + base) + (size_t)kb * (kBlk * kHd * 2), k_off, k_dst);
   };
-  auto issue_v = [&](int kb) {
-    dma_tile8((const char*)(a.v + base) + (size_t)kb * (kBlk * kHd * 2), v_off, v_dst);
+  // Piece i (0..7) of this wave's 8 KiB share of a tile: one 1 KiB DMA. The pieces are spread
+  // between MFMAs: a 16-byte-per-lane DMA holds the issuing wave for tens of cycles, which then
+  // overlaps the previous MFMA instead of stalling a whole phase.
+  auto dma_piece = [&](const char* tile, const uint32_t off[4], uint32_t dst, int i) {
+    const char* src = tile + (i >= 4 ? 4096 : 0);
+    const uint32_t lds = dst + (i >= 4 ? 4096 : 0);
+    switch (i & 3) {
+      case 0: dma_16b<0>(src, off[0], lds); break;
+      case 1: dma_16b<1024>(src, off[1], lds); break;
+      case 2: dma_16b<2048>(src, off[2], lds); break;
+      default: dma_16b<3072>(src, off[3], lds); break;
+    }
   };
+  auto tile_k = [&](int kb) { return (const char*)(a.k + base) + (size_t)kb * (kBlk * kHd * 2); };
+  auto tile_v = [&](int kb) { return (const char*)(a.v + base) + (size_t)kb * (kBlk * kHd * 2); };
 
   // K operand (MFMA A, 32 keys x 16 d): lane reads row 32t + li, logical chunk 2s + lh.
   const char* k_rd = (const char*)k_lds + li * 256;
@@ -520,37 +540,43 @@ void bsa_fwd_dma_kernel(Args a) {
 
   const int nblk = n_off + 1;
   issue_k(key_block(0));
-  issue_v(key_block(0));
-  // vmcnt(0): Q (and the first tiles) have landed. Issued as a real s_waitcnt so the compiler
-  // knows no load of its own is outstanding inside the loop.
+  // vmcnt(0): Q and K(0) have landed. Issued as a real s_waitcnt so the compiler knows no load
+  // of its own is outstanding inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
-  for (int j = 0; j < nblk; ++j) {
-    const bool diag = (j == n_off);
-    USAGI_WAIT_VM(8);  // this wave's K(j) DMA has landed (V(j) may still be in flight)
-    USAGI_BARRIER();
+  // One key block. kDiag: causal mask + no next tile. kMaskQ: some query rows of this block
+  // are past seq_len.
+  auto block = [&](auto diag_tag, auto maskq_tag, int j) {
+    constexpr bool kDiag = decltype(diag_tag)::value;
+    constexpr bool kMaskQ = decltype(maskq_tag)::value;
+    USAGI_WAIT_VM(0);  // this wave's K(j) DMA has landed
+    USAGI_BARRIER();   // K(j) complete; every wave is done reading V(j-1)
+    const char* vt_src = tile_v(key_block(j));
 
+    // ---- S^T = K · Q^T: 32 MFMAs, K operands read 4 ahead.
     floatx16 st[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[t][r] = 0.0f;
     }
+    // V(j) DMA pieces go out between the QK MFMAs (the V buffer is free after the barrier).
+    u32x4 kop[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * (0 ^ k_x));
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int off = 16 * ((2 * s) ^ k_x);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const u32x4 ka = *(const u32x4*)(k_rd + t * 8192 + off);
+        const u32x4 ka = kop[t];
+        if (s < 7) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * ((2 * (s + 1)) ^ k_x));
         st[t] = mfma_qk<false>(ka, qf[s], st[t]);
       }
+      dma_piece(vt_src, v_off, v_dst, s);
     }
 
-    USAGI_WAIT_VM(0);  // V(j) has landed
-    USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
-    if (j + 1 < nblk) issue_k(key_block(j + 1));
-
-    if (diag) {
+    // ---- masks (v7:94, v7:119-122), row max, lazy rescale
+    if constexpr (kDiag) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -559,14 +585,15 @@ void bsa_fwd_dma_kernel(Args a) {
           if (key > q_local || !qvalid) st[t][r] = -INFINITY;
         }
       }
-    } else if (!full_q && !qvalid) {
+    } else if constexpr (kMaskQ) {
+      if (!qvalid) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < 4; ++t) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
+          for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
+        }
       }
     }
-
     float mx = st[0][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -586,44 +613,74 @@ void bsa_fwd_dma_kernel(Args a) {
         for (int r = 0; r < 16; ++r) o_acc[u][r] *= alpha;
       }
     }
+
+    USAGI_WAIT_VM(0);  // V(j) has landed
+    USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
+    const char* kt_src = tile_k(kDiag ? qb : key_block(j + 1));
+
+    // ---- P = exp2(S·scale - m) in fp16, O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
     const float neg_m = -m_used;
-    float psum = 0.0f;
+    half8 pb[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int s = 0; s < 8; ++s) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(st[t][r], scale, neg_m));
-        st[t][r] = p;
-        psum += p;
+      for (int e = 0; e < 8; ++e) {
+        pb[s][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(st[s >> 1][8 * (s & 1) + e], scale, neg_m));
       }
     }
-    l_part += psum;
-
 #pragma unroll
-    for (int hk = 0; hk < 2; ++hk) {  // keys 64hk .. 64hk+63
-      half8 pb[4];
+    for (int s = 0; s < 8; ++s) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pb[s][e] = (_Float16)st[2 * hk + (s >> 1)][8 * (s & 1) + e];
+      for (int u = 0; u < 4; ++u) {
+        const char* vb = v_rd + 16 * (4 * (u ^ tq) + t_x) + s * 4096;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
+        const half8 va = __builtin_shufflevector(__builtin_bit_cast(half4, lo),
+                                                 __builtin_bit_cast(half4, hi), 0, 1, 2, 3, 4, 5, 6, 7);
+        o_acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s], o_acc[u], 0, 0, 0);
       }
+      // K(j+1) DMA pieces between the P·V MFMAs (the K buffer is free after the barrier).
+      if constexpr (!kDiag) dma_piece(kt_src, k_off, k_dst, s);
+    }
+    // Row sum of the fp16 P actually multiplied into V.
+    float psum = l_part;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < 8; ++s) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const char* vb = v_rd + 16 * (4 * (u ^ tq) + t_x) + (4 * hk + s) * 4096;
-          const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
-          const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
-          const half8 va = __builtin_shufflevector(__builtin_bit_cast(half4, lo),
-                                                   __builtin_bit_cast(half4, hi), 0, 1, 2, 3, 4, 5, 6, 7);
-          o_acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s], o_acc[u], 0, 0, 0);
-        }
+      for (int e = 0; e < 4; ++e) {
+        const half2 pp = {pb[s][2 * e], pb[s][2 * e + 1]};
+        psum = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, psum, false);
       }
+    }
+    l_part = psum;
+    // Schedule: 4 V operands (8 transpose reads) in flight, half of the exponentials ahead of
+    // the first MFMA, the rest interleaved with the MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x402, 80, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);
     }
 
     USAGI_BARRIER();  // every wave is done reading V(j)
-    if (j + 1 < nblk) issue_v(key_block(j + 1));
+  };
+
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (full_q) {
+    for (int j = 0; j < n_off; ++j) block(F_{}, F_{}, j);
+  } else {
+    for (int j = 0; j < n_off; ++j) block(F_{}, T_{}, j);
   }
+  block(T_{}, T_{}, n_off);
 
   const float l_tot = wave_pair_sum(l_part);
   float inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;
@@ -647,9 +704,10 @@ void bsa_fwd_dma_kernel(Args a) {
   }
 }
 
+
 thread_local char g_err[512] = "";
 
-// USAGI_BSA_FP16_KERNEL=staged selects the register-staged kernel for fp16 as well (A/B runs).
+// USAGI_BSA_FP16_KERNEL=staged selects the register-staged kernel for fp16 too (A/B runs).
 bool staged_fp16() {
   static const bool v = [] {
     const char* e = getenv("USAGI_BSA_FP16_KERNEL");
