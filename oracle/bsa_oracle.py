@@ -52,11 +52,16 @@ def block_mask(row_ptr_bh: np.ndarray, col_idx_bh: np.ndarray, nqb: int) -> np.n
     return m
 
 
+MUTATIONS = ("scale_1_over_d", "mask_transposed", "drop_diagonal", "k_for_v", "lse_log2")
+
+
 def dense_masked(q, k, v, row_ptr, col_idx, seq_lens=None, dtype=np.float32, slab: int = 1024,
-                 heads: list[tuple[int, int]] | None = None):
+                 heads: list[tuple[int, int]] | None = None, _mutation: str | None = None):
     """fp32 (default) dense-masked attention. Returns (O [B,H,T,D], LSE [B,H,T]) as `dtype`.
 
     `heads` restricts the work to a list of (b, h) pairs (other rows are left as NaN).
+    `_mutation` plants one of MUTATIONS; it exists only so the test suite can show that its
+    pins catch such a mistake.
     """
     qn, kn, vn = _np(q, dtype), _np(k, dtype), _np(v, dtype)
     B, H, T, D = qn.shape
@@ -64,7 +69,7 @@ def dense_masked(q, k, v, row_ptr, col_idx, seq_lens=None, dtype=np.float32, sla
     rp = np.asarray(row_ptr).reshape(B, H, nqb + 1)
     ci = np.asarray(col_idx).reshape(B, H, -1)
     sl = np.full(B, T) if seq_lens is None else np.asarray(seq_lens).reshape(B)
-    scale = dtype(1.0 / math.sqrt(D))
+    scale = dtype(1.0 / math.sqrt(D)) if _mutation != "scale_1_over_d" else dtype(1.0 / D)
     out = np.full((B, H, T, D), np.nan, dtype=dtype)
     lse = np.full((B, H, T), np.nan, dtype=dtype)
     pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
@@ -76,7 +81,12 @@ def dense_masked(q, k, v, row_ptr, col_idx, seq_lens=None, dtype=np.float32, sla
             t1 = min(T, t0 + slab)
             rows = tok[t0:t1]
             mask = bm[rows[:, None] // BLOCK, tok[None, :] // BLOCK]
-            mask &= tok[None, :] <= rows[:, None]
+            if _mutation == "drop_diagonal":
+                mask &= (rows[:, None] // BLOCK) != (tok[None, :] // BLOCK)
+            if _mutation == "mask_transposed":
+                mask &= (tok[None, :] >= rows[:, None]) | ((tok[None, :] // BLOCK) != (rows[:, None] // BLOCK))
+            else:
+                mask &= tok[None, :] <= rows[:, None]
             mask &= tok[None, :] < L
             mask &= (rows < L)[:, None]
             s = (qn[b, h, t0:t1] @ kn[b, h].T) * scale
@@ -86,9 +96,11 @@ def dense_masked(q, k, v, row_ptr, col_idx, seq_lens=None, dtype=np.float32, sla
             mx = np.where(np.isfinite(mx), mx, 0)
             p = np.exp(s - mx)
             l = p.sum(axis=1, keepdims=True)
-            o = (p @ vn[b, h]) / np.where(l > 0, l, 1)
+            vsrc = kn if _mutation == "k_for_v" else vn
+            o = (p @ vsrc[b, h]) / np.where(l > 0, l, 1)
             out[b, h, t0:t1] = np.where(has[:, None], o, 0)
-            lse[b, h, t0:t1] = np.where(has, mx[:, 0] + np.log(np.where(l[:, 0] > 0, l[:, 0], 1)),
+            ln = np.log2 if _mutation == "lse_log2" else np.log
+            lse[b, h, t0:t1] = np.where(has, mx[:, 0] + ln(np.where(l[:, 0] > 0, l[:, 0], 1)),
                                         -np.inf)
     return out, lse
 

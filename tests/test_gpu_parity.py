@@ -95,3 +95,143 @@ def test_bf16_inputs():
     # 2e-3 budget, so rtol = 2e-3 + 2^-9. LSE is fp32 and keeps atol = rtol = 2e-3.
     assert_close(o, oo, rtol=2e-3 + 2.0 ** -9)
     assert_close(lse, ol, what="LSE")
+
+
+# ------------------------------------------------------------------------------ golden fixtures
+
+import os  # noqa: E402
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("name", ["golden_families_t512.npz", "golden_seqlens_t256.npz"])
+def test_golden_fixtures(name):
+    g = np.load(os.path.join(GOLDEN, name))
+    q, k, v = (torch.from_numpy(g[x]) for x in ("q", "k", "v"))
+    print(f"case golden {name}", flush=True)
+    o, lse = run_gpu(q, k, v, g["row_ptr"], g["col_idx"], g["seq_lens"])
+    assert_close(o, g["out"])
+    assert_close(lse, g["lse"], what="LSE")
+
+
+# ------------------------------------------------------------------------------ full-size properties
+
+
+@pytest.fixture(scope="module")
+def full_inputs():
+    B, H, T = 2, 16, 8192
+    q, k, v = (x.to(DEV) for x in P.make_qkv(B, H, T, seed=5))
+    return q, k, v
+
+
+def _dev_csr(name):
+    rp, ci = P.workloads()[name].csr()
+    return torch.from_numpy(rp).to(DEV), torch.from_numpy(ci).to(DEV)
+
+
+@pytest.mark.parametrize("name", ["sliding", "retrieval"])
+def test_full_size_deterministic(full_inputs, name):
+    q, k, v = full_inputs
+    rp, ci = _dev_csr(name)
+    print(f"case determinism {name}", flush=True)
+    o1, l1 = block_sparse_attn_fwd(q, k, v, rp, ci, None)
+    o2, l2 = block_sparse_attn_fwd(q, k, v, rp, ci, None)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+@pytest.mark.parametrize("name", ["global", "retrieval"])
+def test_full_size_linear_in_v(full_inputs, name):
+    """O(2V) = 2 O(V): P is unchanged and scaling by 2 is exact in fp16 and fp32."""
+    q, k, v = full_inputs
+    rp, ci = _dev_csr(name)
+    print(f"case linearity {name}", flush=True)
+    o1, l1 = block_sparse_attn_fwd(q, k, v, rp, ci, None)
+    o2, l2 = block_sparse_attn_fwd(q, k, v * 2, rp, ci, None)
+    torch.cuda.synchronize()
+    assert torch.equal(l1, l2)
+    assert (o2.float() - 2 * o1.float()).abs().max().item() <= 2.0 ** -23
+
+
+def test_full_size_constant_v(full_inputs):
+    q, k, _ = full_inputs
+    rp, ci = _dev_csr("sliding")
+    v = torch.full_like(q, 0.3125)
+    print("case constant V", flush=True)
+    o, lse = block_sparse_attn_fwd(q, k, v, rp, ci, None)
+    torch.cuda.synchronize()
+    assert (o.float() - 0.3125).abs().max().item() <= 2e-3 * 0.3125
+    assert torch.isfinite(lse).all()
+
+
+def test_full_size_head_permutation(full_inputs):
+    """Swapping the data and patterns of two (b, h) pairs swaps their outputs bit for bit."""
+    q, k, v = full_inputs
+    rp, ci = P.workloads()["retrieval"].csr()
+    print("case head permutation", flush=True)
+    o1, l1 = block_sparse_attn_fwd(q, k, v, torch.from_numpy(rp).to(DEV),
+                                   torch.from_numpy(ci).to(DEV), None)
+    perm = lambda x: torch.stack([x[1].flip(0), x[0].flip(0)])  # noqa: E731  (b, h) -> (1-b, H-1-h)
+    rp2 = np.ascontiguousarray(np.stack([rp[1][::-1], rp[0][::-1]]))
+    ci2 = np.ascontiguousarray(np.stack([ci[1][::-1], ci[0][::-1]]))
+    o2, l2 = block_sparse_attn_fwd(perm(q).contiguous(), perm(k).contiguous(), perm(v).contiguous(),
+                                   torch.from_numpy(rp2).to(DEV), torch.from_numpy(ci2).to(DEV), None)
+    torch.cuda.synchronize()
+    assert torch.equal(perm(o1), o2) and torch.equal(perm(l1), l2)
+
+
+# ------------------------------------------------------------------------------ edge cases
+
+
+def test_rows_longer_than_64_blocks():
+    """Rows of up to ~90 key blocks exercise the chunked column-index reload."""
+    B, H, T = 1, 2, 128 * 96
+    rp, ci = P.random_csr(B, H, T, 0.92, 21)
+    assert int(np.diff(rp, axis=-1).max()) > 64
+    q, k, v = P.make_qkv(B, H, T, seed=22)
+    print(f"case long rows T{T} max row {int(np.diff(rp, axis=-1).max())}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    for h in range(H):
+        oo, ol = c_ref.fwd(q[:, h:h + 1].float().numpy(), k[:, h:h + 1].float().numpy(),
+                           v[:, h:h + 1].float().numpy(), rp[:, h:h + 1], ci[:, h:h + 1])
+        assert_close(o[:, h:h + 1], oo, what=f"O[h={h}]")
+        assert_close(lse[:, h:h + 1], ol, what=f"LSE[h={h}]")
+
+
+def test_int64_csr_noncontiguous_inputs_and_list_seq_lens():
+    B, H, T = 2, 3, 640
+    rp, ci = P.retrieval_csr(B, H, T, 3, 4)
+    q, k, v = P.make_qkv(B, H, T, seed=23)
+    print("case int64 csr / non-contiguous", flush=True)
+    # non-contiguous views of the same values: [B, T, H, D] storage transposed to [B, H, T, D]
+    qt, kt, vt = (x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v))
+    assert not qt.is_contiguous()
+    o, lse = block_sparse_attn_fwd(qt, kt, vt, torch.from_numpy(rp.astype(np.int64)).to(DEV),
+                                   torch.from_numpy(ci.astype(np.int64)).to(DEV), [640, 300])
+    torch.cuda.synchronize()
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci, np.array([640, 300]))
+    assert_close(o.float().cpu().numpy(), oo)
+    assert_close(lse.cpu().numpy(), ol, what="LSE")
+
+
+@pytest.mark.parametrize("T", [128, 256])
+def test_single_and_two_block_sequences(T):
+    B, H = 3, 2
+    rp, ci = P.sliding_csr(B, H, T, 2)
+    q, k, v = P.make_qkv(B, H, T, seed=T)
+    print(f"case T={T}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci, [T, T // 2, 1])
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci, np.array([T, T // 2, 1]))
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
+
+
+def test_setup_warms_up():
+    import usagi_amd
+
+    class Spec:
+        def __init__(self, t):
+            self.t_max = t
+
+    print("case setup", flush=True)
+    assert usagi_amd.setup([Spec(1024), Spec(8192), Spec(1024)], "cuda", usagi_amd.VARIANT_MANIFEST) is None

@@ -12,8 +12,10 @@ Differences from the reference, all deliberate:
     instead of a Triton JIT launch; there is no metadata cache keyed on data_ptr()
     (kernels/v7_blockptr_warpspec.py:167-176): int32 contiguous CSR tensors are used in place,
     anything else is converted on every call.
-  * `setup` raises instead of silently returning None when no ROCm device is usable
-    (kernels/v7_blockptr_warpspec.py:202-203), because there is no CPU path.
+  * `setup` loads the ahead-of-time library first, so a missing build fails at setup time; like
+    the reference it returns None without doing anything for a non-GPU device
+    (kernels/v7_blockptr_warpspec.py:202-203), and block_sparse_attn_fwd then rejects CPU
+    tensors (there is no CPU path).
 """
 
 from __future__ import annotations
@@ -115,11 +117,11 @@ def setup(suite_specs, device, variants):
     synchronise). Specs only need a `t_max` attribute.
     """
     _native.load()
+    if str(device) != "cuda" and not str(device).startswith("cuda:"):
+        return None
     if not suite_specs:
         return None
     dev = torch.device(device)
-    if dev.type != "cuda" or not torch.cuda.is_available():
-        raise RuntimeError(f"usagi_amd needs a ROCm GPU device, got {device!r}")
     seen = set()
     for spec in suite_specs:
         T = int(spec.t_max)
