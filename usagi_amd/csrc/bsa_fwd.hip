@@ -10,7 +10,8 @@
 //
 // Two kernels share that structure:
 //   bsa_fwd_dma_kernel      fp16 (the default): K/V tiles DMA'd HBM -> LDS, V read transposed
-//                           out of LDS, two workgroups per CU (see the comment at the kernel).
+//                           out of LDS, two workgroups per CU, diagonal block first (see the
+//                           comment at the kernel).
 //   bsa_fwd_kernel<bf16>    register-staged K/V (global -> VGPR -> LDS, V transposed and
 //                           converted to fp16 on the way in); used for bf16 inputs and, with
 //                           USAGI_BSA_FP16_KERNEL=staged, for fp16 A/B runs.
@@ -366,10 +367,11 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
 // (K: chunk ^ (row % 16), V: chunk ^ 4 * (row % 4)) so that both the DMA writes (1 KiB
 // lane-contiguous per wave instruction) and the MFMA operand reads spread over all banks.
 //
-// Per key block j (three barriers, tiles single-buffered per workgroup, 64 KiB of LDS):
+// Per key block j (two barriers, tiles single-buffered per workgroup, 64 KiB of LDS):
 //   wait K(j) | barrier | S^T = K·Q^T, DMA of V(j) spread between the MFMAs | max, rescale
 //   wait V(j) | barrier | exp2 / fp16 P, O^T += V^T·P^T, DMA of K(j+1) spread between the MFMAs
-//   barrier
+// The diagonal block goes first, so its K tile is requested at entry without reading col_idx.
+// O leaves through LDS as whole rows.
 // A 16-byte-per-lane LDS DMA holds the issuing wave for tens of cycles, so the eight 1 KiB
 // pieces of a wave's share are interleaved with MFMAs instead of being issued back to back.
 // ---------------------------------------------------------------------------------------------
@@ -434,24 +436,50 @@ void bsa_fwd_dma_kernel(Args a) {
   const int qslot = item / a.bh_count;
   const int qb = a.nqb - 1 - qslot;
   const int bh = item - qslot * a.bh_count;
+  const size_t base = (size_t)bh * a.T * kHd;
+  constexpr size_t kTileBytes = (size_t)kBlk * kHd * 2;
+  auto tile_k = [&](int kb) { return (const char*)(a.k + base) + (size_t)kb * kTileBytes; };
+  auto tile_v = [&](int kb) { return (const char*)(a.v + base) + (size_t)kb * kTileBytes; };
+
+  // DMA: wave w, instruction i writes row group 8w + i (rows 32w + 4i + L/16, 1 KiB per wave
+  // instruction). Lane L covers physical chunk L%16 = logical chunk (L%16) ^ swz(row). The
+  // per-lane byte offsets repeat for every tile, so only the uniform tile base changes.
+  const int dma_r = lane >> 4;
+  const int dma_pc = lane & 15;
+  // Row 32w + 4i + L/16 has (row % 16) = 4(i % 4) + L/16 and (row % 4) = L/16.
+  uint32_t k_off[4];
+  uint32_t v_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * i + dma_r)));
+    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * dma_r)));
+  }
+  const uint32_t k_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(k_lds) + wave * 8192);
+  const uint32_t v_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(v_lds) + wave * 8192);
+
+  // The diagonal block is processed first: its key block is qb itself, so its K tile goes out
+  // before anything else is read, while Q, seq_len and the row's column indices are in flight.
+  // (The reference walks it last; online softmax does not depend on the order, up to the fp16
+  // rounding of P.)
+  dma_tile8(tile_k(qb), k_off, k_dst);
+
   const int seq_len = a.seq_lens ? a.seq_lens[bh / a.heads] : a.T;
   const int q0 = qb * kBlk;
-  const size_t base = (size_t)bh * a.T * kHd;
-
   if (q0 >= seq_len) {
+    // The whole query block is past seq_len: O = 0, LSE = -inf (v7:63-67).
     uint16_t* out_blk = a.o + base + (size_t)q0 * kHd;
 #pragma unroll
     for (int i = 0; i < (kBlk * kHd) / (8 * kThreads); ++i) {
       *(u32x4*)(out_blk + (size_t)(i * kThreads + tid) * 8) = u32x4{0, 0, 0, 0};
     }
     if (a.lse && tid < kBlk) a.lse[(size_t)bh * a.T + q0 + tid] = -INFINITY;
+    USAGI_WAIT_VM(0);  // the K tile DMA lands before the workgroup's LDS is released
     return;
   }
 
   const int q_local = wave * 32 + li;
   const int qrow = q0 + q_local;
   const bool qvalid = qrow < seq_len;
-  const bool full_q = q0 + kBlk <= seq_len;
 
   u32x4 qf[8];
   {
@@ -474,7 +502,6 @@ void bsa_fwd_dma_kernel(Args a) {
   int col_chunk = 0;
   int colv = lane < n_off ? cols[lane] : 0;
   auto key_block = [&](int j) -> int {
-    if (j >= n_off) return qb;
     const int c = j >> 6;
     if (c != col_chunk) {
       col_chunk = c;
@@ -485,24 +512,6 @@ void bsa_fwd_dma_kernel(Args a) {
     return min(max(kb, 0), nqb_m1);
   };
 
-  // DMA: wave w, instruction i writes row group 8w + i (rows 32w + 4i + L/16, 1 KiB per wave
-  // instruction). Lane L covers physical chunk L%16 = logical chunk (L%16) ^ swz(row). The
-  // per-lane byte offsets repeat for every tile, so only the uniform tile base changes.
-  const int dma_r = lane >> 4;
-  const int dma_pc = lane & 15;
-  // Row 32w + 4i + L/16 has (row % 16) = 4(i % 4) + L/16 and (row % 4) = L/16.
-  uint32_t k_off[4];
-  uint32_t v_off[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    k_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * i + dma_r)));
-    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * dma_r)));
-  }
-  const uint32_t k_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(k_lds) + wave * 8192);
-  const uint32_t v_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(v_lds) + wave * 8192);
-  auto issue_k = [&](int kb) {
-    dma_tile8((const char*)(a.k + base) + (size_t)kb * (kBlk * kHd * 2), k_off, k_dst);
-  };
   // Piece i (0..7) of this wave's 8 KiB share of a tile: one 1 KiB DMA. The pieces are spread
   // between MFMAs: a 16-byte-per-lane DMA holds the issuing wave for tens of cycles, which then
   // overlaps the previous MFMA instead of stalling a whole phase.
@@ -516,8 +525,6 @@ void bsa_fwd_dma_kernel(Args a) {
       default: dma_16b<3072>(src, off[3], lds); break;
     }
   };
-  auto tile_k = [&](int kb) { return (const char*)(a.k + base) + (size_t)kb * (kBlk * kHd * 2); };
-  auto tile_v = [&](int kb) { return (const char*)(a.v + base) + (size_t)kb * (kBlk * kHd * 2); };
 
   // K operand (MFMA A, 32 keys x 16 d): lane reads row 32t + li, logical chunk 2s + lh.
   const char* k_rd = (const char*)k_lds + li * 256;
@@ -538,22 +545,22 @@ void bsa_fwd_dma_kernel(Args a) {
   float l_part = 0.0f;
   const float scale = a.qk_scale;
 
-  const int nblk = n_off + 1;
-  issue_k(key_block(0));
-  // vmcnt(0): Q and K(0) have landed. Issued as a real s_waitcnt so the compiler knows no load
-  // of its own is outstanding inside the loop.
+  // vmcnt(0): Q, the column chunk and the diagonal K tile have landed. Issued as a real
+  // s_waitcnt so the compiler knows no load of its own is outstanding inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
-  // One key block. kDiag: causal mask + no next tile. kMaskQ: some query rows of this block
-  // are past seq_len.
-  auto block = [&](auto diag_tag, auto maskq_tag, int j) {
+  // One key block: the diagonal (kDiag, j = -1, causal mask) or off-diagonal entry j.
+  // kMaskQ: some query rows of this block are past seq_len. kNext: DMA the K tile of entry
+  // j + 1 during this block's P·V.
+  auto block = [&](auto diag_tag, auto maskq_tag, auto next_tag, int j) {
     constexpr bool kDiag = decltype(diag_tag)::value;
     constexpr bool kMaskQ = decltype(maskq_tag)::value;
+    constexpr bool kNext = decltype(next_tag)::value;
     USAGI_WAIT_VM(0);  // this wave's K(j) DMA has landed
-    USAGI_BARRIER();   // K(j) complete; every wave is done reading V(j-1)
-    const char* vt_src = tile_v(key_block(j));
+    USAGI_BARRIER();   // K(j) complete; every wave is done reading V of the previous block
+    const char* vt_src = tile_v(kDiag ? qb : key_block(j));
 
-    // ---- S^T = K · Q^T: 32 MFMAs, K operands read 4 ahead.
+    // ---- S^T = K · Q^T: 32 MFMAs, K operands read one step ahead.
     floatx16 st[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -574,6 +581,15 @@ void bsa_fwd_dma_kernel(Args a) {
       }
       dma_piece(vt_src, v_off, v_dst, s);
     }
+    // Schedule: each step's 4 K operands are read one step ahead of its 4 MFMAs (deeper
+    // read-ahead only adds registers: the reads complete within one step).
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
 
     // ---- masks (v7:94, v7:119-122), row max, lazy rescale
     if constexpr (kDiag) {
@@ -616,7 +632,7 @@ void bsa_fwd_dma_kernel(Args a) {
 
     USAGI_WAIT_VM(0);  // V(j) has landed
     USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
-    const char* kt_src = tile_k(kDiag ? qb : key_block(j + 1));
+    const char* kt_src = kNext ? tile_k(key_block(j + 1)) : nullptr;
 
     // ---- P = exp2(S·scale - m) in fp16, O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
     const float neg_m = -m_used;
@@ -640,7 +656,7 @@ void bsa_fwd_dma_kernel(Args a) {
         o_acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s], o_acc[u], 0, 0, 0);
       }
       // K(j+1) DMA pieces between the P·V MFMAs (the K buffer is free after the barrier).
-      if constexpr (!kDiag) dma_piece(kt_src, k_off, k_dst, s);
+      if constexpr (kNext) dma_piece(kt_src, k_off, k_dst, s);
     }
     // Row sum of the fp16 P actually multiplied into V.
     float psum = l_part;
@@ -669,33 +685,54 @@ void bsa_fwd_dma_kernel(Args a) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);
     }
-
-    USAGI_BARRIER();  // every wave is done reading V(j)
+    // No closing barrier: the next block's first barrier orders every wave's reads of this V
+    // tile before the DMA of the next one, which is issued after it.
   };
 
   using T_ = std::true_type;
   using F_ = std::false_type;
-  if (full_q) {
-    for (int j = 0; j < n_off; ++j) block(F_{}, F_{}, j);
+  // Off-diagonal blocks use the kMaskQ form even when every query row is valid (the masking
+  // branch is then skipped for the whole wave): separate full-block copies of the block body
+  // push the register allocation of the whole kernel into spills.
+  if (n_off > 0) {
+    block(T_{}, T_{}, T_{}, -1);
+    for (int j = 0; j < n_off - 1; ++j) block(F_{}, T_{}, T_{}, j);
+    block(F_{}, T_{}, F_{}, n_off - 1);
   } else {
-    for (int j = 0; j < n_off; ++j) block(F_{}, T_{}, j);
+    block(T_{}, T_{}, F_{}, -1);
   }
-  block(T_{}, T_{}, n_off);
 
   const float l_tot = wave_pair_sum(l_part);
   float inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;
   if (!qvalid) inv = 0.0f;
-  uint16_t* orow = a.o + base + (size_t)qrow * kHd + 4 * lh;
+  // O: normalise, stage this wave's 32 rows in its 8 KiB slice of the K tile and store whole
+  // 256-byte rows (1 KiB contiguous per instruction); written straight from the accumulator
+  // layout, each store instruction would touch 32 rows with 8 bytes each. The last block DMA'd
+  // no K tile and every wave finished reading its K at that block's second barrier, so the
+  // K tile is free.
+  {
+    char* stage = (char*)k_lds + wave * 8192;  // 32 rows x 256 B, chunk c at c ^ (row % 16)
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 4; ++u) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w[0] = (uint32_t)to_out_bits(o_acc[u][4 * g + 0] * inv, false) |
-             ((uint32_t)to_out_bits(o_acc[u][4 * g + 1] * inv, false) << 16);
-      w[1] = (uint32_t)to_out_bits(o_acc[u][4 * g + 2] * inv, false) |
-             ((uint32_t)to_out_bits(o_acc[u][4 * g + 3] * inv, false) << 16);
-      *(u32x2*)(orow + 32 * u + 8 * g) = w;
+      for (int g = 0; g < 4; ++g) {
+        u32x2 wv;
+        wv[0] = (uint32_t)to_out_bits(o_acc[u][4 * g + 0] * inv, false) |
+                ((uint32_t)to_out_bits(o_acc[u][4 * g + 1] * inv, false) << 16);
+        wv[1] = (uint32_t)to_out_bits(o_acc[u][4 * g + 2] * inv, false) |
+                ((uint32_t)to_out_bits(o_acc[u][4 * g + 3] * inv, false) << 16);
+        // d = 32u + 8g + 4lh .. +3: 16-byte chunk 4u + g, half lh.
+        *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
+      }
+    }
+    // Only this wave's rows: LDS operations of one wave complete in order, no barrier.
+    uint16_t* oblk = a.o + base + (size_t)(q0 + 32 * wave) * kHd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 4 * i + (lane >> 4);
+      const int c = lane & 15;
+      const u32x4 x = *(const u32x4*)(stage + row * 256 + 16 * (c ^ (row & 15)));
+      *(u32x4*)(oblk + (size_t)row * kHd + 8 * c) = x;
     }
   }
   if (a.lse && lh == 0) {
