@@ -70,32 +70,123 @@ def read_traffic():
     return out or None
 
 
-def cpu_baseline(fams, inputs, n_heads: int):
-    """The C port of the reference CSR walk (oracle/bsa_ref.c, OpenMP) on a bounded sample of
-    heads (b = 0, h < n_heads) of each family, projected to the full workload by active
-    blocks."""
-    from oracle import c_ref
+def cpu_baseline(fams, inputs, n_heads: int, c_heads: int):
+    """The reference math as PyTorch CPU fp32 dense-masked attention (oracle/torch_dense.py) on
+    the host cores, per family over heads b < B, h < n_heads (all heads by default: the full
+    workload), projected to B2 H16 by head count when fewer heads are run. The C restatement of
+    the reference's blockwise CSR walk (oracle/bsa_ref.c, OpenMP) is timed beside it on c_heads
+    heads and projected by active blocks."""
+    from oracle import c_ref, torch_dense
 
     q, k, v = inputs
-    qs, ks, vs = (x[:1, :n_heads].float().numpy() for x in (q, k, v))
-    per = {}
+    B, H = q.shape[:2]
+    cores = torch.get_num_threads()
+    heads = [(b, h) for b in range(B) for h in range(min(n_heads, H))]
+    per, per_c = {}, {}
     for name, (rp, ci) in fams.items():
-        rps, cis = rp[:1, :n_heads], ci[:1, :n_heads]
+        rpt, cit = torch.from_numpy(rp), torch.from_numpy(ci)
         t0 = time.perf_counter()
-        c_ref.fwd(qs, ks, vs, rps, cis)
-        dt = time.perf_counter() - t0
-        per[name] = dt * 1e3 * P.active_blocks(rp) / P.active_blocks(rps)
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    return {
+        torch_dense.dense_masked(q, k, v, rpt, cit, heads=heads)
+        per[name] = (time.perf_counter() - t0) * 1e3 * (B * H) / len(heads)
+        if c_heads:
+            qs, ks, vs = (x[:1, :c_heads].float().numpy() for x in (q, k, v))
+            rps, cis = rp[:1, :c_heads], ci[:1, :c_heads]
+            t0 = time.perf_counter()
+            c_ref.fwd(qs, ks, vs, rps, cis)
+            per_c[name] = ((time.perf_counter() - t0) * 1e3 * P.active_blocks(rp)
+                           / P.active_blocks(rps))
+    sample = ("all B2 H16 heads of each family (the full workload)" if len(heads) == B * H else
+              f"heads b<{B}, h<{n_heads} of each family, projected to B2 H16 by head count")
+    out = {
         "value": round(geomean(list(per.values())), 3),
         "unit": "ms",
         "cores": cores,
         "kind": "port",
-        "sample": (f"oracle/bsa_ref.c (C restatement of the reference CSR walk, fp32, OpenMP) on "
-                   f"heads b=0,h<{n_heads} of each family, projected to B2 H16 T8192 by active "
-                   f"blocks; host CPU: {cpu_model()}"),
+        "sample": (f"PyTorch CPU fp32 dense-masked attention (oracle/torch_dense.py: block mask "
+                   f"from the CSR, causal, query slabs of 1024 rows against keys up to the slab "
+                   f"end) on {sample}; geomean over the 3 families of one run each; host CPU: "
+                   f"{cpu_model()}, {cores} threads"),
         "per_family_ms": {k2: round(v2, 3) for k2, v2 in per.items()},
     }
+    if per_c:
+        out["blockwise_c_port"] = {
+            "value": round(geomean(list(per_c.values())), 3),
+            "unit": "ms",
+            "sample": (f"oracle/bsa_ref.c (the reference's CSR walk in C, fp32, OpenMP) on heads "
+                       f"b=0, h<{c_heads}, projected by active blocks"),
+            "per_family_ms": {k2: round(v2, 3) for k2, v2 in per_c.items()},
+        }
+    return out
+
+
+KERNEL = "bsa_fwd_dma_kernel"
+
+
+def pmc_summary(paths, calib_mib: int) -> int:
+    """Per-family averages of rocprofv3 --pmc counters for the attention kernel.
+
+    Dispatches of the kernel come in family order (sliding, global, retrieval) on every warmup
+    and timed step, so dispatch i belongs to FAMILIES[i % 3]. The calibration kernel is the
+    last dispatch before the first attention dispatch (the elementwise -in of
+    --calib-copy-mib MiB, which reads and writes exactly that many bytes); FETCH_SIZE and
+    WRITE_SIZE (KiB) are each scaled by (known KiB / counter KiB) of that kernel.
+    """
+    import csv
+
+    if not calib_mib:
+        print("--pmc-summary needs the --calib-copy-mib value of the profiled run", file=sys.stderr)
+        return 2
+    known_kib = calib_mib * 1024.0
+    sums: dict = {}
+    calib: dict = {}
+    calib_name = None
+    for path in paths:
+        with open(path) as f:
+            rows = list(csv.DictReader(f))
+        by_disp: dict = {}
+        for r in rows:
+            d = int(r["Dispatch_Id"])
+            by_disp.setdefault(d, {"name": r["Kernel_Name"], "ctr": {}})
+            c = by_disp[d]["ctr"]
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        order = sorted(by_disp)
+        first = next(i for i, d in enumerate(order) if KERNEL in by_disp[order[i]]["name"])
+        if first > 0:
+            cal = by_disp[order[first - 1]]
+            calib_name = cal["name"]
+            calib.update(cal["ctr"])
+        i = 0
+        for d in order[first:]:
+            e = by_disp[d]
+            if KERNEL not in e["name"]:
+                continue
+            fam = P.FAMILIES[i % len(P.FAMILIES)]
+            i += 1
+            for cname, val in e["ctr"].items():
+                s = sums.setdefault(fam, {}).setdefault(cname, [0.0, 0])
+                s[0] += val
+                s[1] += 1
+    print(f"kernel {KERNEL}; calibration kernel: {calib_name}")
+    for cname, val in sorted(calib.items()):
+        print(f"calibration {cname} {val:.1f}")
+    factor = {}
+    for cname in ("FETCH_SIZE", "WRITE_SIZE"):
+        if calib.get(cname):
+            factor[cname] = known_kib / calib[cname]
+            print(f"scale {cname} {factor[cname]:.4f}  (known {known_kib:.0f} KiB / counter "
+                  f"{calib[cname]:.1f} KiB)")
+    for fam in P.FAMILIES:
+        if fam not in sums:
+            continue
+        for cname, (tot, n) in sorted(sums[fam].items()):
+            print(f"avg {fam} {cname} {tot / n:.1f}  (over {n} dispatches)")
+        if factor.keys() == {"FETCH_SIZE", "WRITE_SIZE"} and \
+                {"FETCH_SIZE", "WRITE_SIZE"} <= sums[fam].keys():
+            fk = sums[fam]["FETCH_SIZE"][0] / sums[fam]["FETCH_SIZE"][1] * factor["FETCH_SIZE"]
+            wk = sums[fam]["WRITE_SIZE"][0] / sums[fam]["WRITE_SIZE"][1] * factor["WRITE_SIZE"]
+            print(f"traffic_bytes_per_launch {fam} {(fk + wk) * 1024:.0f}  "
+                  f"(read {fk * 1024:.0f} + write {wk * 1024:.0f})")
+    return 0
 
 
 def main() -> int:
@@ -103,13 +194,23 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-heads", type=int, default=4)
+    ap.add_argument("--cpu-heads", type=int, default=16,
+                    help="heads per batch entry timed by the CPU baseline (16 = all)")
+    ap.add_argument("--cpu-c-heads", type=int, default=4,
+                    help="heads timed by the C blockwise port beside it (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=P.INPUT_SEED)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="before the warmup, run one device copy of this many MiB (the known-size "
-                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+                    help="before the warmup, run one elementwise kernel (out = -in, fp32) that "
+                         "reads and writes this many MiB: the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="summarise rocprofv3 --pmc counter_collection.csv files of a run of "
+                         "this script (made with --calib-copy-mib) and exit; no GPU is used")
     args = ap.parse_args()
+
+    if args.pmc_summary:
+        return pmc_summary(args.pmc_summary, args.calib_copy_mib)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU mode "
@@ -138,7 +239,7 @@ def main() -> int:
         src = torch.ones(n, device=dev, dtype=torch.float32)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
 
@@ -194,7 +295,7 @@ def main() -> int:
         "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
         "traffic": (round(sum(traffic[n] for n in P.FAMILIES) / len(P.FAMILIES))
                     if traffic and all(n in traffic for n in P.FAMILIES) else None),
-        "kernel": "bsa_fwd_kernel<fp16>",
+        "kernel": "bsa_fwd_dma_kernel",
         "avg_launch_ms": round(sum(means) / len(means), 4),
         "algorithmic_flop_per_launch": int(sum(flops) / len(flops)),
         "geomean_frac_peak": round(geomean([f["frac_peak"] for f in fam_out.values()]), 4),
@@ -224,7 +325,7 @@ def main() -> int:
         "roofline": roofline,
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(fams, inputs, args.cpu_heads)
+        out["cpu_baseline"] = cpu_baseline(fams, inputs, args.cpu_heads, args.cpu_c_heads)
     print(json.dumps(out), flush=True)
     return 0
 
