@@ -51,6 +51,7 @@ constexpr int kThreads = 256;            // 4 wave64s
 constexpr int kRow = kHd + 8;            // halfs per padded LDS row (272 B)
 constexpr float kTau = 8.0f;             // lazy-rescale threshold, log2 units
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kSpecSum = 4096.0f;      // acceptance bound of a speculative P row sum
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -75,7 +76,29 @@ struct Args {
   int bh_count;
   int max_nnz;
   float qk_scale;  // log2(e) / sqrt(128)
+  int head_major;  // work-item order, see item_coords
 };
+
+// Work item (workgroup index) -> (query block, b*h).
+// head_major == 0: longest rows first over the whole grid (query blocks in descending order,
+//   b*h fastest).
+// head_major == 1 (B*H a multiple of 8): workgroups are dealt to the 8 XCDs round-robin by
+//   index, so item i runs on XCD i % 8; each XCD walks its heads x, x+8, ... one at a time, and
+//   within a head takes the query blocks longest row first. The key/value tiles of the head being
+//   walked (4 MiB at T = 8192) then stay in that XCD's L2 while all its query blocks read them.
+__device__ __forceinline__ void item_coords(const Args& a, int item, int& qb, int& bh) {
+  if (a.head_major) {
+    const int x = item & 7;
+    const int j = item >> 3;
+    const int hl = j / a.nqb;
+    qb = a.nqb - 1 - (j - hl * a.nqb);
+    bh = x + 8 * hl;
+  } else {
+    const int qslot = item / a.bh_count;
+    qb = a.nqb - 1 - qslot;
+    bh = item - qslot * a.bh_count;
+  }
+}
 
 __device__ __forceinline__ float wave_pair_max(float x) {
   // {x[l], x[l ^ 32]} in some order; max is symmetric.
@@ -129,10 +152,8 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
   const int lh = lane >> 5;
 
   // Longest-row-first issue order: descending query block, b*h fastest.
-  const int item = blockIdx.x;
-  const int qslot = item / a.bh_count;
-  const int qb = a.nqb - 1 - qslot;
-  const int bh = item - qslot * a.bh_count;
+  int qb, bh;
+  item_coords(a, blockIdx.x, qb, bh);
   const int seq_len = a.seq_lens ? a.seq_lens[bh / a.heads] : a.T;
   const int q0 = qb * kBlk;
   const size_t base = (size_t)bh * a.T * kHd;
@@ -420,6 +441,7 @@ __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
 
 #define USAGI_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 #define USAGI_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+#define USAGI_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bsa_fwd_dma_kernel(Args a) {
@@ -432,10 +454,8 @@ void bsa_fwd_dma_kernel(Args a) {
   const int li = lane & 31;
   const int lh = lane >> 5;
 
-  const int item = blockIdx.x;
-  const int qslot = item / a.bh_count;
-  const int qb = a.nqb - 1 - qslot;
-  const int bh = item - qslot * a.bh_count;
+  int qb, bh;
+  item_coords(a, blockIdx.x, qb, bh);
   const size_t base = (size_t)bh * a.T * kHd;
   constexpr size_t kTileBytes = (size_t)kBlk * kHd * 2;
   auto tile_k = [&](int kb) { return (const char*)(a.k + base) + (size_t)kb * kTileBytes; };
@@ -610,40 +630,73 @@ void bsa_fwd_dma_kernel(Args a) {
         }
       }
     }
-    float mx = st[0][0];
+    // ---- P = exp2(S·scale - m) in fp16 and its row sum (this lane's 64 keys).
+    // The diagonal block (always the first block of a row) takes the exact row max. Later blocks
+    // compute P with the running max as it stands: each P is <= the lane's fp32 sum of its P,
+    // so a sum <= 2^12 proves every P finite in fp16 and the result exact in the normalised
+    // output; otherwise (rare) the row max moves to the block's exact max, O and l are rescaled
+    // and P recomputed.
+    half8 pb[8];
+    float pblk = 0.0f;
+    auto make_p = [&]() {
+      const float neg_m = -m_used;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+      for (int s = 0; s < 8; ++s) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
-    }
-    mx = wave_pair_max(mx);
-    const float m_cand = fmaxf(m_used, mx * scale);
-    const bool grow = m_cand > m_used + kTau;
-    if (__any(grow)) {
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_used - m_cand) : 1.0f;
-      m_used = grow ? m_cand : m_used;
+        for (int e = 0; e < 8; ++e) {
+          pb[s][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(st[s >> 1][8 * (s & 1) + e], scale, neg_m));
+        }
+      }
+      float acc = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2 pp = {pb[s][2 * e], pb[s][2 * e + 1]};
+          acc = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, acc, false);
+        }
+      }
+      pblk = acc;
+    };
+    auto row_max = [&]() {
+      float mx = st[0][0];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
+      }
+      return wave_pair_max(mx);
+    };
+    auto rescale = [&](float m_new) {
+      const float alpha = __builtin_amdgcn_exp2f(m_used - m_new);
+      m_used = m_new;
       l_part *= alpha;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o_acc[u][r] *= alpha;
       }
+    };
+    if constexpr (kDiag) {
+      const float m_new = fmaxf(m_used, row_max() * scale);
+      if (__any(m_new > m_used)) rescale(m_new);
+      make_p();
+    } else {
+      make_p();
+      asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]), "v"(pb[4]), "v"(pb[5]),
+                   "v"(pb[6]), "v"(pb[7]));
+      if (__builtin_expect(__any(!(pblk <= kSpecSum)), 0)) {
+        rescale(fmaxf(m_used, row_max() * scale));
+        make_p();
+      }
     }
+    l_part += pblk;
 
     USAGI_WAIT_VM(0);  // V(j) has landed
     USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
     const char* kt_src = kNext ? tile_k(key_block(j + 1)) : nullptr;
 
-    // ---- P = exp2(S·scale - m) in fp16, O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
-    const float neg_m = -m_used;
-    half8 pb[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pb[s][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(st[s >> 1][8 * (s & 1) + e], scale, neg_m));
-      }
-    }
+    // ---- O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
@@ -658,32 +711,11 @@ void bsa_fwd_dma_kernel(Args a) {
       // K(j+1) DMA pieces between the P·V MFMAs (the K buffer is free after the barrier).
       if constexpr (kNext) dma_piece(kt_src, k_off, k_dst, s);
     }
-    // Row sum of the fp16 P actually multiplied into V.
-    float psum = l_part;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const half2 pp = {pb[s][2 * e], pb[s][2 * e + 1]};
-        psum = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, psum, false);
-      }
-    }
-    l_part = psum;
-    // Schedule: 4 V operands (8 transpose reads) in flight, half of the exponentials ahead of
-    // the first MFMA, the rest interleaved with the MFMAs.
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-    __builtin_amdgcn_sched_group_barrier(0x402, 80, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 32; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 2, 0);
     }
     // No closing barrier: the next block's first barrier orders every wave's reads of this V
     // tile before the DMA of the next one, which is issued after it.
@@ -741,14 +773,567 @@ void bsa_fwd_dma_kernel(Args a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp16 split kernel: one workgroup per CU (4 waves, one per SIMD), K/V double-buffered in LDS.
+//
+// Wave w = (rw, cw) = (w / 2, w % 2) owns query rows 64 rw .. 64 rw + 63 and keys
+// 64 cw .. 64 cw + 63 of every key block. Every K or V^T operand a wave reads from LDS feeds two
+// MFMAs (one per 32-row query fragment f), so LDS reads per FLOP are half of the 32-row layout.
+// The two waves of a row pair keep separate online-softmax states over their key halves; the
+// states are merged once, in the epilogue (m = max, O and l rescaled by 2^(m_i - m)).
+//
+// Tiles: stage s holds K and V of one key block (2 x 32 KiB); the DMA of block p+1 goes to the
+// other stage during block p, so each tile is requested a whole block ahead. One barrier per
+// block. Inside a block each wave works in 32-key sub-tiles t:
+//   QK(t0) [16 MFMAs, next block's 16 DMA pieces between them]
+//   QK(t1) [16 MFMAs] alongside exp2 of sub-tile 0 computed with the running max
+//   row max over the 64 keys; if it grew by more than 2^8 anywhere (rare after the first block):
+//   rescale O, l and recompute sub-tile 0's P
+//   PV(t0) [16 MFMAs] alongside exp2 of sub-tile 1
+//   PV(t1) [16 MFMAs]
+// The diagonal block goes first (non-speculative, causally masked; waves with cw > rw have no
+// key at or before any of their query rows there and skip it).
+// Query rows at or past seq_len are computed like the others and written as O = 0, LSE = -inf
+// at the end: off-diagonal keys and causally visible diagonal keys of a valid row are all before
+// seq_len, so no other mask is needed.
+// ---------------------------------------------------------------------------------------------
+
+// Multiplies an MFMA accumulator that lives in AGPRs by alpha, in place. Written with AGPR
+// operands so the compiler never copies the accumulators into VGPRs for it: a plain multiply on
+// a rarely taken path makes it read all of them out of the AGPRs on every loop iteration.
+__device__ __forceinline__ void scale_acc_agpr(floatx16& acc, float alpha) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = acc[r];
+    float t;
+    asm volatile(
+        "v_accvgpr_read_b32 %1, %0\n\t"
+        "v_mul_f32 %1, %1, %2\n\t"
+        "v_accvgpr_write_b32 %0, %1"
+        : "+a"(x), "=&v"(t)
+        : "v"(alpha));
+    acc[r] = x;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void bsa_fwd_split_kernel(Args a) {
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[4 * kBlk * kHd];  // [stage][K | V]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = wave >> 1;
+  const int cw = wave & 1;
+  const int li = lane & 31;
+  const int lh = lane >> 5;
+
+  int qb, bh;
+  item_coords(a, blockIdx.x, qb, bh);
+  const size_t base = (size_t)bh * a.T * kHd;
+  constexpr size_t kTileBytes = (size_t)kBlk * kHd * 2;
+  auto tile_k = [&](int kb) { return (const char*)(a.k + base) + (size_t)kb * kTileBytes; };
+  auto tile_v = [&](int kb) { return (const char*)(a.v + base) + (size_t)kb * kTileBytes; };
+
+  // DMA: wave w moves tile rows 32w .. 32w+31 (8 x 1 KiB), swizzled as in bsa_fwd_dma_kernel.
+  const int dma_r = lane >> 4;
+  const int dma_pc = lane & 15;
+  uint32_t k_off[4];
+  uint32_t v_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * i + dma_r)));
+    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * dma_r)));
+  }
+  const uint32_t lds0 = lds_addr_of(lds);
+  auto k_dst = [&](int stage) {
+    return __builtin_amdgcn_readfirstlane(lds0 + 65536u * stage + wave * 8192);
+  };
+  auto v_dst = [&](int stage) {
+    return __builtin_amdgcn_readfirstlane(lds0 + 65536u * stage + 32768u + wave * 8192);
+  };
+
+  dma_tile8(tile_k(qb), k_off, k_dst(0));
+  dma_tile8(tile_v(qb), v_off, v_dst(0));
+
+  const int seq_len = a.seq_lens ? a.seq_lens[bh / a.heads] : a.T;
+  const int q0 = qb * kBlk;
+  if (q0 >= seq_len) {
+    uint16_t* out_blk = a.o + base + (size_t)q0 * kHd;
+#pragma unroll
+    for (int i = 0; i < (kBlk * kHd) / (8 * kThreads); ++i) {
+      *(u32x4*)(out_blk + (size_t)(i * kThreads + tid) * 8) = u32x4{0, 0, 0, 0};
+    }
+    if (a.lse && tid < kBlk) a.lse[(size_t)bh * a.T + q0 + tid] = -INFINITY;
+    USAGI_WAIT_VM(0);
+    return;
+  }
+
+  // Q^T fragments (MFMA B operand): qf[f][s] = Q[q0 + 64 rw + 32 f + li][16 s + 8 lh .. +8].
+  u32x4 qf[2][8];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const uint16_t* qp = a.q + base + (size_t)(q0 + 64 * rw + 32 * f + li) * kHd + 8 * lh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[f][s] = *(const u32x4*)(qp + 16 * s);
+  }
+
+  const int32_t* rp = a.row_ptr + (size_t)bh * (a.nqb + 1) + qb;
+  int rs = rp[0];
+  int re = rp[1];
+  rs = min(max(rs, 0), a.max_nnz);
+  re = min(max(re, rs), a.max_nnz);
+  const int n_off = max(re - rs - 1, 0);
+  const int32_t* cols = a.col_idx + (size_t)bh * a.max_nnz + rs;
+  const int nqb_m1 = a.nqb - 1;
+  int col_chunk = 0;
+  int colv = lane < n_off ? cols[lane] : 0;
+  auto key_block = [&](int j) -> int {
+    const int c = j >> 6;
+    if (c != col_chunk) {
+      col_chunk = c;
+      const int e = c * 64 + lane;
+      colv = e < n_off ? cols[e] : 0;
+    }
+    const int kb = __builtin_amdgcn_readlane(colv, j & 63);
+    return min(max(kb, 0), nqb_m1);
+  };
+
+  auto dma_piece = [&](const char* tile, const uint32_t off[4], uint32_t dst, int i) {
+    const char* src = tile + (i >= 4 ? 4096 : 0);
+    const uint32_t l = dst + (i >= 4 ? 4096 : 0);
+    switch (i & 3) {
+      case 0: dma_16b<0>(src, off[0], l); break;
+      case 1: dma_16b<1024>(src, off[1], l); break;
+      case 2: dma_16b<2048>(src, off[2], l); break;
+      default: dma_16b<3072>(src, off[3], l); break;
+    }
+  };
+
+  // LDS read addresses (bytes, relative to a stage): K operand rows 64 cw + 32 t + li, logical
+  // chunk 2 s + lh at physical chunk (2 s + lh) ^ (li % 16).
+  const int k_rd = (64 * cw + li) * 256;
+  const int k_x = lh ^ (li & 15);
+  // V^T operand via transpose reads (as in bsa_fwd_dma_kernel), global k-step S = 4 cw + 2 t + s2.
+  const int tq = (lane & 15) >> 2;
+  const int t_x = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int v_rd = 32768 + (4 * lh + tq) * 256 + 8 * (lane & 1) + cw * 4 * 4096;
+  const char* lds_c = (const char*)lds;
+
+  floatx16 o_acc[4][2];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o_acc[u][f][r] = 0.0f;
+    }
+  }
+  float m_used[2] = {-1e30f, -1e30f};
+  float l_part[2] = {0.0f, 0.0f};
+  const float scale = a.qk_scale;
+
+  auto k_op = [&](int stage, int t, int s) -> u32x4 {
+    return *(const u32x4*)(lds_c + stage * 65536 + k_rd + t * 8192 + 16 * ((2 * s) ^ k_x));
+  };
+  auto v_op = [&](int stage, int t, int s2, int u) -> half8 {
+    const char* vb = lds_c + stage * 65536 + v_rd + 16 * (4 * (u ^ tq) + t_x) + (2 * t + s2) * 4096;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
+    return __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // P of sub-tile t as two k-steps x two query fragments (MFMA B operands).
+  auto exp_tile = [&](const floatx16 (&s)[2], half8 (&p)[2][2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const float neg_m = -m_used[f];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          p[s2][f][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[f][8 * s2 + e], scale, neg_m));
+        }
+      }
+    }
+  };
+  auto psum = [&](const half8 (&p)[2][2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      float acc = l_part[f];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const half2 pp = {p[s2][f][2 * e], p[s2][f][2 * e + 1]};
+          acc = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, acc, false);
+        }
+      }
+      l_part[f] = acc;
+    }
+  };
+  auto qk_tile = [&](int stage, int t, floatx16 (&s)[2]) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[f][r] = 0.0f;
+    }
+#pragma unroll
+    for (int ss = 0; ss < 8; ++ss) {
+      const u32x4 ka = k_op(stage, t, ss);
+      s[0] = mfma_qk<false>(ka, qf[0][ss], s[0]);
+      s[1] = mfma_qk<false>(ka, qf[1][ss], s[1]);
+    }
+  };
+  auto pv_tile = [&](int stage, int t, const half8 (&p)[2][2]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const half8 va = v_op(stage, t, s2, u);
+        o_acc[u][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, p[s2][0], o_acc[u][0], 0, 0, 0);
+        o_acc[u][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, p[s2][1], o_acc[u][1], 0, 0, 0);
+      }
+    }
+  };
+  auto tile_max = [&](const floatx16& s) {
+    float mx = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    return mx;
+  };
+
+  // vmcnt(0): Q, the column chunk and the diagonal tiles have landed.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  USAGI_BARRIER();
+
+  // ---- the diagonal block (stage 0); the first off-diagonal block's tiles go to stage 1.
+  if (n_off > 0) {
+    const int kb = key_block(0);
+    dma_tile8(tile_k(kb), k_off, k_dst(1));
+    dma_tile8(tile_v(kb), v_off, v_dst(1));
+  }
+  if (cw <= rw) {
+    floatx16 s0[2], s1[2];
+    qk_tile(0, 0, s0);
+    qk_tile(0, 1, s1);
+    if (cw == rw) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (key > 32 * f + li) s0[f][r] = -INFINITY;
+          if (32 + key > 32 * f + li) s1[f][r] = -INFINITY;
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const float mx = wave_pair_max(fmaxf(tile_max(s0[f]), tile_max(s1[f])));
+      m_used[f] = fmaxf(m_used[f], mx * scale);
+    }
+    half8 p0[2][2], p1[2][2];
+    exp_tile(s0, p0);
+    exp_tile(s1, p1);
+    pv_tile(0, 0, p0);
+    pv_tile(0, 1, p1);
+    psum(p0);
+    psum(p1);
+  }
+
+  // ---- off-diagonal blocks: processing index p = 1 .. n_off is CSR entry p - 1, stage p % 2.
+  //
+  // The body is written as explicit steps separated by scheduling fences
+  // (__builtin_amdgcn_sched_barrier(0)): each step issues the LDS operand read two steps ahead,
+  // its MFMAs, and a chunk of VALU work that does not depend on them, so the matrix core runs
+  // while the wave computes exponentials. Without the fences the compiler groups all DMAs, all
+  // reads and all MFMAs and sinks the speculative exponentials past the rescale test.
+  int koff[8];
+#pragma unroll
+  for (int ss = 0; ss < 8; ++ss) koff[ss] = k_rd + 16 * ((2 * ss) ^ k_x);
+  int voff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) voff[u] = v_rd + 16 * (4 * (u ^ tq) + t_x);
+
+  // Four elements of sub-tile sv (chunk c = 0..7: query fragment c / 4, elements 4 (c % 4) ..)
+  // -> fp16 P with the running max as it stands, and their row sum into sum[f].
+  auto exp_chunk = [&](const floatx16 (&sv)[2], half8 (&p)[2][2], float (&sum)[2], int c) {
+    const int f = c >> 2;
+    const int j0 = 4 * (c & 3);
+    const int s2 = j0 >> 3;
+    const int e0 = j0 & 7;
+    const float neg_m = -m_used[f];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[s2][f][e0 + e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sv[f][j0 + e], scale, neg_m));
+    }
+    float acc = sum[f];
+    acc = __builtin_amdgcn_fdot2(half2{p[s2][f][e0], p[s2][f][e0 + 1]}, half2{1.0f16, 1.0f16}, acc, false);
+    acc = __builtin_amdgcn_fdot2(half2{p[s2][f][e0 + 2], p[s2][f][e0 + 3]}, half2{1.0f16, 1.0f16}, acc, false);
+    sum[f] = acc;
+  };
+  // A sub-tile's P was computed with the running max as it stands. Every P is <= the lane's
+  // fp32 sum of its 16 P values, so a sum <= 2^12 proves all of them finite in fp16 and the
+  // speculation good (and it is, for almost every block after the first). Otherwise (rare) take
+  // the exact row max of the sub-tile, move the running max to it, rescale O and l, and
+  // recompute the sub-tile's P and sum. Then the sum joins l.
+  auto check = [&](const floatx16 (&sv)[2], half8 (&p)[2][2], float (&sum)[2]) {
+    // The speculative P is consumed here, so the compiler cannot sink its computation past the
+    // branch (into the common path after the MFMAs it was meant to overlap).
+    asm volatile("" ::"v"(p[0][0]), "v"(p[0][1]), "v"(p[1][0]), "v"(p[1][1]));
+    const bool big = !(sum[0] <= kSpecSum) || !(sum[1] <= kSpecSum);
+    if (__builtin_expect(__any(big), 0)) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const float mx = wave_pair_max(tile_max(sv[f]));
+        const float m_new = fmaxf(m_used[f], mx * scale);
+        const float alpha = __builtin_amdgcn_exp2f(m_used[f] - m_new);
+        m_used[f] = m_new;
+        l_part[f] *= alpha;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) scale_acc_agpr(o_acc[u][f], alpha);
+      }
+      exp_tile(sv, p);
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            acc = __builtin_amdgcn_fdot2(half2{p[s2][f][e], p[s2][f][e + 1]}, half2{1.0f16, 1.0f16}, acc, false);
+          }
+        }
+        sum[f] = acc;
+      }
+    }
+    l_part[0] += sum[0];
+    l_part[1] += sum[1];
+  };
+
+  auto block = [&](auto next_tag, int p) {
+    constexpr bool kNext = decltype(next_tag)::value;
+    const int stage = p & 1;
+    USAGI_WAIT_VM(0);  // this wave's share of block p's tiles has landed
+    USAGI_BARRIER();   // every share has landed; every wave is done with block p - 1
+    const char* nk = nullptr;
+    const char* nv = nullptr;
+    uint32_t nkd = 0, nvd = 0;
+    if constexpr (kNext) {
+      const int kb = key_block(p);
+      nk = tile_k(kb);
+      nv = tile_v(kb);
+      nkd = k_dst(stage ^ 1);
+      nvd = v_dst(stage ^ 1);
+    }
+    const char* st_base = lds_c + stage * 65536;
+    auto kread = [&](int t, int ss) -> u32x4 {
+      return *(const u32x4*)(st_base + koff[ss] + t * 8192);
+    };
+    auto vread = [&](int t, int s2, int u) -> half8 {
+      const char* vb = st_base + voff[u] + (2 * t + s2) * 4096;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
+      return __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi),
+                                     0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    floatx16 s0[2], s1[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s0[f][r] = 0.0f;
+        s1[f][r] = 0.0f;
+      }
+    }
+
+    // A: QK(t0) with the next block's K tile DMA (one 1 KiB piece per two MFMAs).
+    u32x4 kA = kread(0, 0);
+    u32x4 kB = kread(0, 1);
+    USAGI_FENCE();
+#pragma unroll
+    for (int ss = 0; ss < 8; ++ss) {
+      const u32x4 kN = ss < 6 ? kread(0, ss + 2) : kread(1, ss - 6);
+      s0[0] = mfma_qk<false>(kA, qf[0][ss], s0[0]);
+      if constexpr (kNext) dma_piece(nk, k_off, nkd, ss);
+      s0[1] = mfma_qk<false>(kA, qf[1][ss], s0[1]);
+      kA = kB;
+      kB = kN;
+      USAGI_FENCE();
+    }
+
+    // B: QK(t1) with sub-tile 0's P (speculative: the running max as it stands) and row sums.
+    half8 p0[2][2];
+    float sum0[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int ss = 0; ss < 8; ++ss) {
+      u32x4 kN = kB;
+      if (ss < 6) kN = kread(1, ss + 2);
+      s1[0] = mfma_qk<false>(kA, qf[0][ss], s1[0]);
+      exp_chunk(s0, p0, sum0, ss);
+      s1[1] = mfma_qk<false>(kA, qf[1][ss], s1[1]);
+      kA = kB;
+      kB = kN;
+      USAGI_FENCE();
+    }
+    check(s0, p0, sum0);
+
+    // D: PV(t0) with sub-tile 1's P and row sums.
+    half8 p1[2][2];
+    float sum1[2] = {0.0f, 0.0f};
+    half8 vA = vread(0, 0, 0);
+    half8 vB = vread(0, 0, 1);
+    USAGI_FENCE();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s2 = i >> 2;
+      const int u = i & 3;
+      const half8 vN = i < 6 ? vread(0, (i + 2) >> 2, (i + 2) & 3) : vread(1, 0, i - 6);
+      o_acc[u][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vA, p0[s2][0], o_acc[u][0], 0, 0, 0);
+      exp_chunk(s1, p1, sum1, i);
+      o_acc[u][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vA, p0[s2][1], o_acc[u][1], 0, 0, 0);
+      vA = vB;
+      vB = vN;
+      USAGI_FENCE();
+    }
+    check(s1, p1, sum1);
+
+    // E: PV(t1) with the next block's V tile DMA (one piece per two MFMAs).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s2 = i >> 2;
+      const int u = i & 3;
+      half8 vN = vB;
+      if (i < 6) vN = vread(1, (i + 2) >> 2, (i + 2) & 3);
+      o_acc[u][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vA, p1[s2][0], o_acc[u][0], 0, 0, 0);
+      if constexpr (kNext) dma_piece(nv, v_off, nvd, i);
+      o_acc[u][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vA, p1[s2][1], o_acc[u][1], 0, 0, 0);
+      vA = vB;
+      vB = vN;
+      USAGI_FENCE();
+    }
+  };
+
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  for (int p = 1; p < n_off; ++p) block(T_{}, p);
+  if (n_off > 0) block(F_{}, n_off);
+
+  // ---- epilogue: merge the two key halves of each row pair, normalise, store.
+  USAGI_BARRIER();  // every wave is done with the tiles; the LDS is reused below
+  float l_tot[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) l_tot[f] = wave_pair_sum(l_part[f]);
+  // Wave (rw, cw) keeps d-tiles u = 2 cw, 2 cw + 1 and hands the other two to its partner:
+  // region (rw, cw) = 16 KiB at 32 KiB rw + 16 KiB cw, float index (i * 64 + lane) with
+  // i = ((u % 2) * 2 + f) * 16 + r; m and l at 64 KiB + 1 KiB (2 rw + cw).
+  {
+    // (register arrays are only ever indexed with compile-time indices: a run-time index would
+    // move o_acc to scratch memory)
+    float* xo = (float*)(lds_c + rw * 32768 + cw * 16384);
+#pragma unroll
+    for (int uu = 0; uu < 2; ++uu) {
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          xo[((uu * 2 + f) * 16 + r) * 64 + lane] = cw ? o_acc[uu][f][r] : o_acc[2 + uu][f][r];
+        }
+      }
+    }
+    float* xm = (float*)(lds_c + 65536 + 1024 * (2 * rw + cw));
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      xm[f * 64 + lane] = m_used[f];
+      xm[128 + f * 64 + lane] = l_tot[f];
+    }
+  }
+  USAGI_BARRIER();
+  const float* po = (const float*)(lds_c + rw * 32768 + (1 - cw) * 16384);
+  const float* pm = (const float*)(lds_c + 65536 + 1024 * (2 * rw + (1 - cw)));
+  float inv[2], a0[2], a1[2], m_fin[2], l_fin[2];
+  bool qv[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const float mp = pm[f * 64 + lane];
+    const float lp = pm[128 + f * 64 + lane];
+    const float mn = fmaxf(m_used[f], mp);
+    a0[f] = __builtin_amdgcn_exp2f(m_used[f] - mn);
+    a1[f] = __builtin_amdgcn_exp2f(mp - mn);
+    const float l = l_tot[f] * a0[f] + lp * a1[f];
+    m_fin[f] = mn;
+    l_fin[f] = l;
+    qv[f] = q0 + 64 * rw + 32 * f + li < seq_len;
+    inv[f] = l > 0.0f ? 1.0f / l : 1.0f;
+  }
+  // Stage this wave's 64 rows x 64 d (128 B per row) at 72 KiB + 8 KiB wave, 16-byte chunk c of
+  // row r at c ^ (r % 8); then store whole 128-byte row halves.
+  char* stage_o = (char*)lds_c + 73728 + wave * 8192;
+#pragma unroll
+  for (int uu = 0; uu < 2; ++uu) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int row = 32 * f + li;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          // Rows past seq_len were computed on whatever their Q holds: select, never multiply.
+          const float own = cw ? o_acc[2 + uu][f][r] : o_acc[uu][f][r];
+          const float x = (own * a0[f] + po[((uu * 2 + f) * 16 + r) * 64 + lane] * a1[f]) * inv[f];
+          v[e] = qv[f] ? x : 0.0f;
+        }
+        u32x2 wv;
+        wv[0] = (uint32_t)to_out_bits(v[0], false) | ((uint32_t)to_out_bits(v[1], false) << 16);
+        wv[1] = (uint32_t)to_out_bits(v[2], false) | ((uint32_t)to_out_bits(v[3], false) << 16);
+        const int chunk = 4 * uu + g;  // d_local = 32 uu + 8 g + 4 lh
+        *(u32x2*)(stage_o + row * 128 + 16 * (chunk ^ (row & 7)) + 8 * lh) = wv;
+      }
+    }
+  }
+  // Only this wave's rows: LDS operations of one wave complete in order, no barrier.
+  uint16_t* oblk = a.o + base + (size_t)(q0 + 64 * rw) * kHd + 64 * cw;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 8 * i + (lane >> 3);
+    const int c = lane & 7;
+    const u32x4 x = *(const u32x4*)(stage_o + row * 128 + 16 * (c ^ (row & 7)));
+    *(u32x4*)(oblk + (size_t)row * kHd + 8 * c) = x;
+  }
+  if (a.lse && cw == 0 && lh == 0) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int qrow = q0 + 64 * rw + 32 * f + li;
+      const float lse = (qv[f] && l_fin[f] > 0.0f) ? (m_fin[f] + log2f(l_fin[f])) * kLn2 : -INFINITY;
+      a.lse[(size_t)bh * a.T + qrow] = lse;
+    }
+  }
+}
+
 
 thread_local char g_err[512] = "";
 
-// USAGI_BSA_FP16_KERNEL=staged selects the register-staged kernel for fp16 too (A/B runs).
-bool staged_fp16() {
-  static const bool v = [] {
+// USAGI_BSA_FP16_KERNEL selects the fp16 kernel for A/B runs: "dma" (default), "split" or
+// "staged" (the register-staged kernel that bf16 uses).
+int fp16_kernel() {
+  static const int v = [] {
     const char* e = getenv("USAGI_BSA_FP16_KERNEL");
-    return e && strcmp(e, "staged") == 0;
+    if (e && strcmp(e, "staged") == 0) return 2;
+    if (e && strcmp(e, "split") == 0) return 0;
+    return 1;
+  }();
+  return v;
+}
+
+// USAGI_BSA_ORDER=rows forces the longest-row-first grid order (A/B runs); default: head-major
+// per XCD whenever B*H is a multiple of 8.
+int item_order() {
+  static const int v = [] {
+    const char* e = getenv("USAGI_BSA_ORDER");
+    return (e && strcmp(e, "rows") == 0) ? 0 : 1;
   }();
   return v;
 }
@@ -803,16 +1388,19 @@ extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
   a.bh_count = (int)bh;
   a.max_nnz = max_nnz;
   a.qk_scale = (float)(1.4426950408889634 / sqrt((double)kHd));
+  a.head_major = (bh % 8 == 0 && item_order() != 0) ? 1 : 0;
 
   const dim3 grid((unsigned)(bh * nqb));
   const dim3 block(kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == USAGI_BSA_BF16) {
     hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
-  } else if (staged_fp16()) {
+  } else if (fp16_kernel() == 2) {
     hipLaunchKernelGGL(bsa_fwd_kernel<false>, grid, block, 0, s, a);
-  } else {
+  } else if (fp16_kernel() == 1) {
     hipLaunchKernelGGL(bsa_fwd_dma_kernel, grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(bsa_fwd_split_kernel, grid, block, 0, s, a);
   }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
