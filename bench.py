@@ -10,7 +10,10 @@ D=128, fp16, plus the fraction of dense fp16 MFMA peak counting only active 128x
 A step is one forward call of each family on synthetic inputs already resident in HBM. Every
 call is bracketed by HIP events on the launch stream; the per-family median gives the latency.
 
-    python bench.py [--steps K] [--warmup W] [--cpu-heads N | --no-cpu]
+    python bench.py [--steps K] [--warmup W] [--min-warmup-s S] [--cpu-heads N | --no-cpu]
+
+The warmup is W steps plus, if needed, more whole steps until S seconds have passed (reported as
+warmup_extra_steps): from idle the GPU takes tens of ms of sustained load to reach steady clocks.
 
 Prints one JSON line.
 """
@@ -193,7 +196,11 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=150)
+    ap.add_argument("--min-warmup-s", type=float, default=0.3,
+                    help="keep warming up (whole steps) until this much wall time has passed: the "
+                         "GPU needs a few tens of ms of sustained load to reach its steady clocks, "
+                         "and the first calls after idle run up to 20%% slower")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads per batch entry timed by the CPU baseline (16 = all)")
     ap.add_argument("--cpu-c-heads", type=int, default=4,
@@ -251,6 +258,14 @@ def main() -> int:
         for name in P.FAMILIES:
             call(name)
     torch.cuda.synchronize()
+    extra = 0
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < args.min_warmup_s and args.min_warmup_s > 0:
+        for _ in range(10):
+            for name in P.FAMILIES:
+                call(name)
+            extra += 1
+        torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
     ev = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -308,6 +323,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_extra_steps": extra,
         "ms_per_step": round(wall * 1e3 / args.steps, 4),
         "higher_is_better": False,
         "scaling": "weak",

@@ -580,6 +580,10 @@ void bsa_fwd_dma_kernel(Args a) {
     USAGI_BARRIER();   // K(j) complete; every wave is done reading V of the previous block
     const char* vt_src = tile_v(kDiag ? qb : key_block(j));
 
+    // Matrix-core sections run at raised wave priority, so when both waves of a SIMD (one per
+    // workgroup) can issue, the MFMA stream goes first and the other wave's exponentials fill
+    // the gaps.
+    __builtin_amdgcn_s_setprio(1);
     // ---- S^T = K · Q^T: 32 MFMAs, K operands read one step ahead.
     floatx16 st[4];
 #pragma unroll
@@ -591,13 +595,17 @@ void bsa_fwd_dma_kernel(Args a) {
     u32x4 kop[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * (0 ^ k_x));
+    // On the diagonal, key tile t (keys 32t .. 32t+31) lies above every row of wave w when t > w:
+    // those tiles are skipped (their scores stay 0 and are masked below).
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const u32x4 ka = kop[t];
-        if (s < 7) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * ((2 * (s + 1)) ^ k_x));
-        st[t] = mfma_qk<false>(ka, qf[s], st[t]);
+        if (!kDiag || t <= wave) {
+          const u32x4 ka = kop[t];
+          if (s < 7) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * ((2 * (s + 1)) ^ k_x));
+          st[t] = mfma_qk<false>(ka, qf[s], st[t]);
+        }
       }
       dma_piece(vt_src, v_off, v_dst, s);
     }
@@ -630,6 +638,7 @@ void bsa_fwd_dma_kernel(Args a) {
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---- P = exp2(S·scale - m) in fp16 and its row sum (this lane's 64 keys).
     // The diagonal block (always the first block of a row) takes the exact row max. Later blocks
     // compute P with the running max as it stands: each P is <= the lane's fp32 sum of its P,
@@ -696,11 +705,14 @@ void bsa_fwd_dma_kernel(Args a) {
     USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
     const char* kt_src = kNext ? tile_k(key_block(j + 1)) : nullptr;
 
+    __builtin_amdgcn_s_setprio(1);
     // ---- O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
+        // Diagonal: k-step s holds keys 16s .. 16s+15, all above wave w's rows when s > 2w + 1.
+        if (kDiag && s > 2 * wave + 1) continue;
         const char* vb = v_rd + 16 * (4 * (u ^ tq) + t_x) + s * 4096;
         const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
         const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
@@ -717,6 +729,7 @@ void bsa_fwd_dma_kernel(Args a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     // No closing barrier: the next block's first barrier orders every wave's reads of this V
     // tile before the DMA of the next one, which is issued after it.
   };
@@ -749,10 +762,12 @@ void bsa_fwd_dma_kernel(Args a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 wv;
-        wv[0] = (uint32_t)to_out_bits(o_acc[u][4 * g + 0] * inv, false) |
-                ((uint32_t)to_out_bits(o_acc[u][4 * g + 1] * inv, false) << 16);
-        wv[1] = (uint32_t)to_out_bits(o_acc[u][4 * g + 2] * inv, false) |
-                ((uint32_t)to_out_bits(o_acc[u][4 * g + 3] * inv, false) << 16);
+        // Rows past seq_len were computed on whatever their Q holds: select, never multiply.
+        float ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = qvalid ? o_acc[u][4 * g + e] * inv : 0.0f;
+        wv[0] = (uint32_t)to_out_bits(ov[0], false) | ((uint32_t)to_out_bits(ov[1], false) << 16);
+        wv[1] = (uint32_t)to_out_bits(ov[2], false) | ((uint32_t)to_out_bits(ov[3], false) << 16);
         // d = 32u + 8g + 4lh .. +3: 16-byte chunk 4u + g, half lh.
         *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
       }
