@@ -235,3 +235,61 @@ def test_setup_warms_up():
 
     print("case setup", flush=True)
     assert usagi_amd.setup([Spec(1024), Spec(8192), Spec(1024)], "cuda", usagi_amd.VARIANT_MANIFEST) is None
+
+
+# ------------------------------------------------------------------------------ running-max growth
+
+
+def _growth_inputs(seed):
+    """Scores of key block 0 far above the diagonal block's: the running max taken on the
+    diagonal (processed first) is then exceeded by far more than the fp16 range of P in a later
+    block, which must take the exact-max rescale path. Also a case with every score sharpened."""
+    B, H, T = 1, 2, 768
+    rp, ci = P.global_csr(B, H, T, 1, 2)  # every row: key block 0, previous block, diagonal
+    q, k, v = P.make_qkv(B, H, T, seed=seed)
+    k = k.clone()
+    k[:, :, :128] *= 6.0  # key block 0: scores up to ~6x the rest
+    return q, k, v, rp, ci
+
+
+@pytest.mark.parametrize("kernel", ["dma", "split", "staged"])
+def test_running_max_growth_takes_the_rescale_path(kernel, monkeypatch):
+    monkeypatch.setenv("USAGI_BSA_FP16_KERNEL", kernel)
+    q, k, v, rp, ci = _growth_inputs(31)
+    print(f"case growth kernel={kernel}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
+
+
+@pytest.mark.parametrize("kernel", ["dma", "split"])
+def test_sharp_softmax(kernel, monkeypatch):
+    """q and k scaled by 3: scores 9x the unit-variance case (near one-hot rows)."""
+    monkeypatch.setenv("USAGI_BSA_FP16_KERNEL", kernel)
+    B, H, T = 1, 2, 1024
+    rp, ci = P.retrieval_csr(B, H, T, 5, 3)
+    q, k, v = P.make_qkv(B, H, T, seed=32)
+    q, k = (q.float() * 3.0).half(), (k.float() * 3.0).half()
+    print(f"case sharp kernel={kernel}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
+
+
+@pytest.mark.parametrize("kernel", ["split"])
+@pytest.mark.parametrize("name", ["sliding", "retrieval"])
+def test_other_fp16_kernels_full_size_heads(kernel, name, monkeypatch):
+    """The selectable fp16 kernels against the C walk on three heads at full size."""
+    monkeypatch.setenv("USAGI_BSA_FP16_KERNEL", kernel)
+    w = P.workloads()[name]
+    rp, ci = w.csr()
+    q, k, v = P.make_qkv(w.B, w.H, w.T, seed=6)
+    print(f"case {kernel} {name}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    for b, h in [(0, 0), (w.B - 1, w.H - 1), (0, w.H // 2)]:
+        qs, ks, vs = (x[b:b + 1, h:h + 1].float().numpy() for x in (q, k, v))
+        oo, ol = c_ref.fwd(qs, ks, vs, rp[b:b + 1, h:h + 1], ci[b:b + 1, h:h + 1])
+        assert_close(o[b:b + 1, h:h + 1], oo, what=f"O[{b},{h}]")
+        assert_close(lse[b:b + 1, h:h + 1], ol, what=f"LSE[{b},{h}]")

@@ -1332,25 +1332,19 @@ void bsa_fwd_split_kernel(Args a) {
 thread_local char g_err[512] = "";
 
 // USAGI_BSA_FP16_KERNEL selects the fp16 kernel for A/B runs: "dma" (default), "split" or
-// "staged" (the register-staged kernel that bf16 uses).
+// "staged" (the register-staged kernel that bf16 uses); read on every call.
 int fp16_kernel() {
-  static const int v = [] {
-    const char* e = getenv("USAGI_BSA_FP16_KERNEL");
-    if (e && strcmp(e, "staged") == 0) return 2;
-    if (e && strcmp(e, "split") == 0) return 0;
-    return 1;
-  }();
-  return v;
+  const char* e = getenv("USAGI_BSA_FP16_KERNEL");
+  if (e && strcmp(e, "staged") == 0) return 2;
+  if (e && strcmp(e, "split") == 0) return 0;
+  return 1;
 }
 
 // USAGI_BSA_ORDER=rows forces the longest-row-first grid order (A/B runs); default: head-major
 // per XCD whenever B*H is a multiple of 8.
 int item_order() {
-  static const int v = [] {
-    const char* e = getenv("USAGI_BSA_ORDER");
-    return (e && strcmp(e, "rows") == 0) ? 0 : 1;
-  }();
-  return v;
+  const char* e = getenv("USAGI_BSA_ORDER");
+  return (e && strcmp(e, "rows") == 0) ? 0 : 1;
 }
 
 int fail(int code, const char* fmt, ...) {
