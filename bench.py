@@ -133,6 +133,12 @@ def pmc_summary(paths, calib_mib: int) -> int:
     last dispatch before the first attention dispatch (the elementwise -in of
     --calib-copy-mib MiB, which reads and writes exactly that many bytes); FETCH_SIZE and
     WRITE_SIZE (KiB) are each scaled by (known KiB / counter KiB) of that kernel.
+
+    When a pass also ran with --kernel-trace, its run_kernel_trace.csv (next to the counter
+    file) gives each dispatch's duration, and run_agent_info.csv the part's XCD and SIMD
+    counts; the derived lines then put the counters against time: the shader clock
+    (GRBM_GUI_ACTIVE is summed over the XCDs), MFMA busy share, TFLOP/s on active blocks and
+    the fraction of the MFMA peak at that clock, HBM GB/s and the LDS bank-conflict rate.
     """
     import csv
 
@@ -141,8 +147,10 @@ def pmc_summary(paths, calib_mib: int) -> int:
         return 2
     known_kib = calib_mib * 1024.0
     sums: dict = {}
+    durs: dict = {}
     calib: dict = {}
     calib_name = None
+    n_xcc, n_simd = 8, 1024
     for path in paths:
         with open(path) as f:
             rows = list(csv.DictReader(f))
@@ -152,6 +160,18 @@ def pmc_summary(paths, calib_mib: int) -> int:
             by_disp.setdefault(d, {"name": r["Kernel_Name"], "ctr": {}})
             c = by_disp[d]["ctr"]
             c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        trace = path.replace("counter_collection", "kernel_trace")
+        dur_of: dict = {}
+        if trace != path and os.path.exists(trace):
+            with open(trace) as f:
+                for r in csv.DictReader(f):
+                    dur_of[int(r["Dispatch_Id"])] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        agent = path.replace("counter_collection", "agent_info")
+        if agent != path and os.path.exists(agent):
+            with open(agent) as f:
+                for r in csv.DictReader(f):
+                    if r.get("Name", "").startswith("gfx"):
+                        n_xcc, n_simd = int(r["Num_Xcc"]), int(r["Simd_Count"])
         order = sorted(by_disp)
         first = next(i for i, d in enumerate(order) if KERNEL in by_disp[order[i]]["name"])
         if first > 0:
@@ -169,6 +189,10 @@ def pmc_summary(paths, calib_mib: int) -> int:
                 s = sums.setdefault(fam, {}).setdefault(cname, [0.0, 0])
                 s[0] += val
                 s[1] += 1
+            if d in dur_of:
+                t = durs.setdefault(fam, [0.0, 0])
+                t[0] += dur_of[d]
+                t[1] += 1
     print(f"kernel {KERNEL}; calibration kernel: {calib_name}")
     for cname, val in sorted(calib.items()):
         print(f"calibration {cname} {val:.1f}")
@@ -178,17 +202,47 @@ def pmc_summary(paths, calib_mib: int) -> int:
             factor[cname] = known_kib / calib[cname]
             print(f"scale {cname} {factor[cname]:.4f}  (known {known_kib:.0f} KiB / counter "
                   f"{calib[cname]:.1f} KiB)")
+    wl = P.workloads()
     for fam in P.FAMILIES:
         if fam not in sums:
             continue
+        avg = {cname: tot / n for cname, (tot, n) in sums[fam].items()}
         for cname, (tot, n) in sorted(sums[fam].items()):
             print(f"avg {fam} {cname} {tot / n:.1f}  (over {n} dispatches)")
+        traffic = None
         if factor.keys() == {"FETCH_SIZE", "WRITE_SIZE"} and \
-                {"FETCH_SIZE", "WRITE_SIZE"} <= sums[fam].keys():
-            fk = sums[fam]["FETCH_SIZE"][0] / sums[fam]["FETCH_SIZE"][1] * factor["FETCH_SIZE"]
-            wk = sums[fam]["WRITE_SIZE"][0] / sums[fam]["WRITE_SIZE"][1] * factor["WRITE_SIZE"]
-            print(f"traffic_bytes_per_launch {fam} {(fk + wk) * 1024:.0f}  "
+                {"FETCH_SIZE", "WRITE_SIZE"} <= avg.keys():
+            fk = avg["FETCH_SIZE"] * factor["FETCH_SIZE"]
+            wk = avg["WRITE_SIZE"] * factor["WRITE_SIZE"]
+            traffic = (fk + wk) * 1024
+            print(f"traffic_bytes_per_launch {fam} {traffic:.0f}  "
                   f"(read {fk * 1024:.0f} + write {wk * 1024:.0f})")
+        if fam not in durs:
+            continue
+        dur_ns = durs[fam][0] / durs[fam][1]
+        flop = P.active_blocks(wl[fam].csr()[0]) * 4 * P.BLOCK ** 3
+        tflops = flop / dur_ns / 1e3
+        print(f"derived {fam} duration_us {dur_ns / 1e3:.1f}  (kernel trace of the counter passes, "
+              f"{durs[fam][1]} dispatches)  tflops_active {tflops:.1f}")
+        if avg.get("GRBM_GUI_ACTIVE"):
+            cyc = avg["GRBM_GUI_ACTIVE"] / n_xcc
+            ghz = cyc / dur_ns
+            peak_at_clock = ghz * 1e9 * n_simd * 1024 / 1e12  # 1024 fp16 FLOP/clk per SIMD
+            print(f"derived {fam} clock_ghz {ghz:.3f}  (GRBM_GUI_ACTIVE / {n_xcc} XCDs / duration)  "
+                  f"mfma_peak_at_clock_tflops {peak_at_clock:.0f}  "
+                  f"frac_of_peak_at_clock {tflops / peak_at_clock:.3f}")
+            if avg.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None:
+                print(f"derived {fam} mfma_busy {avg['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * n_simd):.3f}  "
+                      f"(SQ_VALU_MFMA_BUSY_CYCLES / ({n_simd} SIMDs x cycles))")
+        if avg.get("SQ_VALU_MFMA_COEXEC_CYCLES") is not None and avg.get("SQ_VALU_MFMA_BUSY_CYCLES"):
+            print(f"derived {fam} valu_coexec_share_of_mfma_busy "
+                  f"{avg['SQ_VALU_MFMA_COEXEC_CYCLES'] / avg['SQ_VALU_MFMA_BUSY_CYCLES']:.3f}")
+        if avg.get("SQ_LDS_IDX_ACTIVE") and "SQ_LDS_BANK_CONFLICT" in avg:
+            print(f"derived {fam} lds_bank_conflict_rate "
+                  f"{avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_LDS_IDX_ACTIVE']:.4f}  "
+                  f"(SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE)")
+        if traffic is not None:
+            print(f"derived {fam} hbm_gbs {traffic / dur_ns:.0f}")
     return 0
 
 

@@ -1,0 +1,97 @@
+"""bench.py --pmc-summary on synthetic rocprofv3 CSVs with known answers (CPU only).
+
+The counter values are chosen so every derived figure has a closed form: a calibration kernel
+that reads half its known size in FETCH_SIZE (scale 2) and all of it in WRITE_SIZE (scale 1), then
+three attention dispatches (one per family) with fixed counters and durations.
+"""
+import csv
+import os
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, REPO)
+
+from usagi_amd import patterns as P  # noqa: E402
+
+KERNEL = "(anonymous namespace)::bsa_fwd_dma_kernel((anonymous namespace)::Args)"
+CALIB = "vectorized_elementwise_kernel<neg>"
+
+
+def _write(dirpath, with_trace=True):
+    ctr = os.path.join(dirpath, "run_counter_collection.csv")
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    rows = []
+    calib_kib = 256 * 1024
+    rows += [(1, CALIB, "FETCH_SIZE", calib_kib / 2), (1, CALIB, "WRITE_SIZE", calib_kib),
+             (1, CALIB, "GRBM_GUI_ACTIVE", 1000.0), (1, CALIB, "SQ_VALU_MFMA_BUSY_CYCLES", 0.0),
+             (1, CALIB, "SQ_LDS_BANK_CONFLICT", 0.0), (1, CALIB, "SQ_LDS_IDX_ACTIVE", 1.0)]
+    for k, fam in enumerate(P.FAMILIES):
+        d = 2 + k
+        # 8 XCDs x 200000 cycles in 100 us -> 2.0 GHz; MFMA busy half of 1024 SIMDs x 200000
+        rows += [(d, KERNEL, "FETCH_SIZE", 100000.0), (d, KERNEL, "WRITE_SIZE", 50000.0),
+                 (d, KERNEL, "GRBM_GUI_ACTIVE", 8 * 200000.0),
+                 (d, KERNEL, "SQ_VALU_MFMA_BUSY_CYCLES", 0.5 * 1024 * 200000.0),
+                 (d, KERNEL, "SQ_LDS_BANK_CONFLICT", 10.0), (d, KERNEL, "SQ_LDS_IDX_ACTIVE", 1000.0)]
+    with open(ctr, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(fields)
+        w.writerows(rows)
+    if with_trace:
+        with open(os.path.join(dirpath, "run_kernel_trace.csv"), "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+            w.writerow([1, CALIB, 0, 5000])
+            for k in range(3):
+                w.writerow([2 + k, KERNEL, 10_000_000 * (k + 1), 10_000_000 * (k + 1) + 100_000])
+        with open(os.path.join(dirpath, "run_agent_info.csv"), "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(["Name", "Num_Xcc", "Simd_Count", "Cu_Count"])
+            w.writerow(["gfx950", 8, 1024, 256])
+    return ctr
+
+
+def _run(ctr):
+    out = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--pmc-summary", ctr,
+                          "--calib-copy-mib", "256"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    return out.stdout
+
+
+def _field(text, key, fam, name):
+    for line in text.splitlines():
+        parts = line.split()
+        if len(parts) >= 4 and parts[0] == key and parts[1] == fam:
+            for a, b in zip(parts[2:], parts[3:]):
+                if a == name:
+                    return float(b)
+    raise AssertionError(f"{key} {fam} {name} missing in:\n{text}")
+
+
+def test_traffic_scaled_by_the_calibration_kernel(tmp_path):
+    text = _run(_write(str(tmp_path), with_trace=False))
+    for fam in P.FAMILIES:
+        # (100000 KiB x 2 + 50000 KiB x 1) x 1024
+        line = next(l for l in text.splitlines() if l.startswith(f"traffic_bytes_per_launch {fam} "))
+        assert float(line.split()[2]) == pytest.approx(250000 * 1024)
+    assert "derived" not in text  # no kernel trace: no time-based figures
+
+
+def test_derived_figures_against_closed_forms(tmp_path):
+    text = _run(_write(str(tmp_path)))
+    wl = P.workloads()
+    for fam in P.FAMILIES:
+        assert _field(text, "derived", fam, "duration_us") == pytest.approx(100.0)
+        flop = P.active_blocks(wl[fam].csr()[0]) * 4 * 128 ** 3
+        tf = _field(text, "derived", fam, "tflops_active")
+        assert tf == pytest.approx(flop / 100e-6 / 1e12, rel=1e-3)
+        assert _field(text, "derived", fam, "clock_ghz") == pytest.approx(2.0)
+        # peak at 2.0 GHz: 1024 SIMDs x 1024 FLOP/clk
+        assert _field(text, "derived", fam, "mfma_peak_at_clock_tflops") == pytest.approx(2097, abs=1)
+        assert _field(text, "derived", fam, "frac_of_peak_at_clock") == pytest.approx(
+            tf / (2.0e9 * 1024 * 1024 / 1e12), abs=1e-3)
+        assert _field(text, "derived", fam, "mfma_busy") == pytest.approx(0.5)
+        assert _field(text, "derived", fam, "lds_bank_conflict_rate") == pytest.approx(0.01)
+        assert _field(text, "derived", fam, "hbm_gbs") == pytest.approx(250000 * 1024 / 100e3, rel=1e-3)
