@@ -84,17 +84,38 @@ def test_random_csr(seed):
     assert_close(lse, ol, what="LSE")
 
 
-def test_bf16_inputs():
+# O is stored in bf16 for bf16 inputs: its rounding (up to half an ulp, 2^-9 relative) comes on
+# top of the 2e-3 budget, so rtol = 2e-3 + 2^-9. LSE is fp32 and keeps atol = rtol = 2e-3.
+BF16_RTOL = 2e-3 + 2.0 ** -9
+
+
+@pytest.mark.parametrize("kernel", ["dma", "staged"])
+def test_bf16_inputs(kernel, monkeypatch):
+    monkeypatch.setenv("USAGI_BSA_FP16_KERNEL", kernel)
     B, H, T = 1, 2, 1024
     rp, ci = P.retrieval_csr(B, H, T, 5, 7)
     q, k, v = P.make_qkv(B, H, T, seed=4, dtype=torch.bfloat16)
-    print("case bf16", flush=True)
+    print(f"case bf16 kernel={kernel}", flush=True)
     o, lse = run_gpu(q, k, v, rp, ci)
     oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
-    # O is stored in bf16: its rounding (up to half an ulp, 2^-9 relative) comes on top of the
-    # 2e-3 budget, so rtol = 2e-3 + 2^-9. LSE is fp32 and keeps atol = rtol = 2e-3.
-    assert_close(o, oo, rtol=2e-3 + 2.0 ** -9)
+    assert_close(o, oo, rtol=BF16_RTOL)
     assert_close(lse, ol, what="LSE")
+
+
+@pytest.mark.parametrize("name", ["sliding", "retrieval"])
+def test_bf16_full_size_heads_vs_c_oracle(name):
+    """bf16 inputs at the full sizes (the default kernel) against the C walk on three heads."""
+    w = P.workloads()[name]
+    rp, ci = w.csr()
+    q, k, v = P.make_qkv(w.B, w.H, w.T, seed=7, dtype=torch.bfloat16)
+    print(f"case bf16 {name} B{w.B} H{w.H} T{w.T}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    for b, h in [(0, 0), (w.B - 1, w.H - 1), (0, w.H // 2)]:
+        qs, ks, vs = (x[b:b + 1, h:h + 1].float().numpy() for x in (q, k, v))
+        oo, ol = c_ref.fwd(qs, ks, vs, rp[b:b + 1, h:h + 1], ci[b:b + 1, h:h + 1])
+        assert_close(o[b:b + 1, h:h + 1], oo, rtol=BF16_RTOL, what=f"O[{b},{h}]")
+        assert_close(lse[b:b + 1, h:h + 1], ol, what=f"LSE[{b},{h}]")
 
 
 # ------------------------------------------------------------------------------ golden fixtures
@@ -260,6 +281,17 @@ def test_running_max_growth_takes_the_rescale_path(kernel, monkeypatch):
     o, lse = run_gpu(q, k, v, rp, ci)
     oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
     assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
+
+
+def test_bf16_running_max_growth():
+    """The rescale path with bf16 inputs (default kernel)."""
+    q, k, v, rp, ci = _growth_inputs(33)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    print("case growth bf16", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo, rtol=BF16_RTOL)
     assert_close(lse, ol, what="LSE")
 
 

@@ -443,6 +443,7 @@ __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
 #define USAGI_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define USAGI_FENCE() __builtin_amdgcn_sched_barrier(0)
 
+template <bool kBf16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bsa_fwd_dma_kernel(Args a) {
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kBlk * kHd];  // K[key][d], swizzled
@@ -604,7 +605,7 @@ void bsa_fwd_dma_kernel(Args a) {
         if (!kDiag || t <= wave) {
           const u32x4 ka = kop[t];
           if (s < 7) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * ((2 * (s + 1)) ^ k_x));
-          st[t] = mfma_qk<false>(ka, qf[s], st[t]);
+          st[t] = mfma_qk<kBf16>(ka, qf[s], st[t]);
         }
       }
       dma_piece(vt_src, v_off, v_dst, s);
@@ -702,6 +703,26 @@ void bsa_fwd_dma_kernel(Args a) {
     l_part += pblk;
 
     USAGI_WAIT_VM(0);  // V(j) has landed
+    if constexpr (kBf16) {
+      // bf16 inputs: this wave turns its own 8 KiB of the V tile (the rows its DMA wrote) into
+      // fp16 in place before the barrier publishes the tile, so P·V runs on fp16 P and fp16 V as
+      // the reference's does (v7:107). Element positions do not matter: every 16-bit value is
+      // converted where it lies.
+      char* slice = (char*)v_lds + wave * 8192 + lane * 16;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = *(const u32x4*)(slice + (4 * h + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) x[i][w] = bf16x2_to_f16x2(x[i][w]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *(u32x4*)(slice + (4 * h + i) * 1024) = x[i];
+      }
+    }
     USAGI_BARRIER();   // every wave is done reading K(j); V(j) is complete
     const char* kt_src = kNext ? tile_k(key_block(j + 1)) : nullptr;
 
@@ -766,8 +787,8 @@ void bsa_fwd_dma_kernel(Args a) {
         float ov[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) ov[e] = qvalid ? o_acc[u][4 * g + e] * inv : 0.0f;
-        wv[0] = (uint32_t)to_out_bits(ov[0], false) | ((uint32_t)to_out_bits(ov[1], false) << 16);
-        wv[1] = (uint32_t)to_out_bits(ov[2], false) | ((uint32_t)to_out_bits(ov[3], false) << 16);
+        wv[0] = (uint32_t)to_out_bits(ov[0], kBf16) | ((uint32_t)to_out_bits(ov[1], kBf16) << 16);
+        wv[1] = (uint32_t)to_out_bits(ov[2], kBf16) | ((uint32_t)to_out_bits(ov[3], kBf16) << 16);
         // d = 32u + 8g + 4lh .. +3: 16-byte chunk 4u + g, half lh.
         *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
       }
@@ -1331,8 +1352,9 @@ void bsa_fwd_split_kernel(Args a) {
 
 thread_local char g_err[512] = "";
 
-// USAGI_BSA_FP16_KERNEL selects the fp16 kernel for A/B runs: "dma" (default), "split" or
-// "staged" (the register-staged kernel that bf16 uses); read on every call.
+// USAGI_BSA_FP16_KERNEL selects the kernel for A/B runs, read on every call: "dma" (default,
+// fp16 and bf16), "split" (fp16 only; bf16 inputs stay on "dma") or "staged" (the
+// register-staged kernel, fp16 and bf16).
 int fp16_kernel() {
   const char* e = getenv("USAGI_BSA_FP16_KERNEL");
   if (e && strcmp(e, "staged") == 0) return 2;
@@ -1403,11 +1425,15 @@ extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
   const dim3 block(kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == USAGI_BSA_BF16) {
-    hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
+    if (fp16_kernel() == 2) {
+      hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
+    } else {
+      hipLaunchKernelGGL(bsa_fwd_dma_kernel<true>, grid, block, 0, s, a);
+    }
   } else if (fp16_kernel() == 2) {
     hipLaunchKernelGGL(bsa_fwd_kernel<false>, grid, block, 0, s, a);
   } else if (fp16_kernel() == 1) {
-    hipLaunchKernelGGL(bsa_fwd_dma_kernel, grid, block, 0, s, a);
+    hipLaunchKernelGGL(bsa_fwd_dma_kernel<false>, grid, block, 0, s, a);
   } else {
     hipLaunchKernelGGL(bsa_fwd_split_kernel, grid, block, 0, s, a);
   }
