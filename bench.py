@@ -35,7 +35,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
-from usagi_amd import block_sparse_attn_fwd  # noqa: E402
+from usagi_amd import block_sparse_attn_fwd, block_sparse_attn_fwd_window  # noqa: E402
 from usagi_amd import patterns as P  # noqa: E402
 
 METRIC = "geomean fwd ms @B2 H16 T8192 D128 over 3 sparsity families; % fp16 MFMA peak"
@@ -378,6 +378,33 @@ def main() -> int:
     for name in P.FAMILIES:
         fam_out[name]["launch_ms"] = round(launch_ms[name], 4)
     mean_launch = sum(launch_ms.values()) / len(launch_ms)
+
+    # Analytic rows (no CSR, block_sparse_attn_fwd_window) for the families that are a window or
+    # a window plus a global prefix, call by call against the CSR path for a like-for-like ratio.
+    analytic = {}
+    for name in P.FAMILIES:
+        ex = wl[name].extra
+        if "window" not in ex:
+            continue
+        ev_w = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.steps)]
+        ev_c = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.steps)]
+        for s in range(args.steps):
+            a, b = ev_w[s]
+            a.record(stream)
+            block_sparse_attn_fwd_window(q, k, v, ex["window"], ex["n_global"])
+            b.record(stream)
+            a, b = ev_c[s]
+            a.record(stream)
+            call(name)
+            b.record(stream)
+        torch.cuda.synchronize()
+        mw = float(np.median([a.elapsed_time(b) for a, b in ev_w]))
+        mc = float(np.median([a.elapsed_time(b) for a, b in ev_c]))
+        analytic[name] = {"window": ex["window"], "n_global": ex["n_global"],
+                          "median_ms": round(mw, 4), "csr_median_ms": round(mc, 4),
+                          "ratio_to_csr": round(mw / mc, 4)}
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
     roofline = {
@@ -417,6 +444,7 @@ def main() -> int:
             "families": fam_out,
             "latency_timing": "HIP events around each call on the launch stream; median over "
                               "the timed steps per family",
+            "analytic_rows": analytic,
             "input_seed": args.seed,
             "pattern_seed": P.PATTERN_SEED,
         },

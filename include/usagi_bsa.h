@@ -60,6 +60,18 @@ int usagi_bsa_fwd(const void* q, const void* k, const void* v,
                   int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
                   int32_t max_nnz, int32_t dtype, void* stream);
 
+/* Forward pass over an analytic pattern instead of a CSR: query block qb attends the global
+ * prefix 0 .. n_global-1 and the window max(0, qb-window+1) .. qb (deduplicated; the diagonal is
+ * causally masked), with no row_ptr / col_idx reads. Same tensors, dtype, seq_lens, lse, stream
+ * and return conventions as usagi_bsa_fwd; the result equals usagi_bsa_fwd on the CSR of that
+ * pattern. Replaces the analytic kernels _fwd_window (window only) and _fwd_window_global of
+ * kernels/v1_baseline.py:141-322. window >= 1, n_global >= 0. */
+int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
+                         int32_t window, int32_t n_global, const int32_t* seq_lens,
+                         void* out, float* lse,
+                         int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
+                         int32_t dtype, void* stream);
+
 /* Host-side CSR validator over HOST copies of row_ptr / col_idx. It checks the preconditions
  * under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-111 equals
  * block-mask ∧ causal attention: row_ptr[0] == 0, monotone, row_ptr[nqb] <= max_nnz, every row

@@ -325,3 +325,57 @@ def test_other_fp16_kernels_full_size_heads(kernel, name, monkeypatch):
         oo, ol = c_ref.fwd(qs, ks, vs, rp[b:b + 1, h:h + 1], ci[b:b + 1, h:h + 1])
         assert_close(o[b:b + 1, h:h + 1], oo, what=f"O[{b},{h}]")
         assert_close(lse[b:b + 1, h:h + 1], ol, what=f"LSE[{b},{h}]")
+
+
+# ------------------------------------------------------------------------------ analytic rows
+
+
+def run_gpu_window(q, k, v, window, n_global, sl=None):
+    from usagi_amd import block_sparse_attn_fwd_window
+
+    dq, dk, dv = (x.to(DEV) for x in (q, k, v))
+    dsl = None if sl is None else torch.as_tensor(np.asarray(sl, dtype=np.int32)).to(DEV)
+    o, lse = block_sparse_attn_fwd_window(dq, dk, dv, window, n_global, dsl)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), lse.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,H,T,w,g", [
+    (1, 2, 1024, 4, 0), (1, 2, 1024, 3, 2), (1, 2, 1024, 1, 0), (1, 2, 1024, 1, 3),
+    (1, 2, 1024, 100, 0), (1, 2, 1024, 2, 100), (2, 16, 8192, 8, 0), (2, 16, 8192, 4, 4),
+])
+def test_window_path_equals_csr_path_bitwise(B, H, T, w, g):
+    """The analytic rows walk the same blocks in the same order as the CSR of the pattern, so
+    O and LSE are bit-identical (the full-size cases are the sliding and global families)."""
+    rp, ci = P.global_csr(B, H, T, g, w) if g else P.sliding_csr(B, H, T, w)
+    q, k, v = P.make_qkv(B, H, T, seed=41)
+    print(f"case window w={w} g={g} B{B} H{H} T{T}", flush=True)
+    o_csr, lse_csr = run_gpu(q, k, v, rp, ci)
+    o_win, lse_win = run_gpu_window(q, k, v, w, g)
+    assert np.array_equal(o_win, o_csr)
+    assert np.array_equal(lse_win, lse_csr)
+
+
+@pytest.mark.parametrize("seq_lens", [[1024, 700], [0, 1000], [128, 1]])
+def test_window_path_vs_dense_oracle(seq_lens):
+    B, H, T, w, g = 2, 2, 1024, 3, 2
+    rp, ci = P.global_csr(B, H, T, g, w)
+    q, k, v = P.make_qkv(B, H, T, seed=42)
+    print(f"case window oracle seq_lens={seq_lens}", flush=True)
+    o, lse = run_gpu_window(q, k, v, w, g, seq_lens)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci, np.array(seq_lens))
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
+
+
+def test_window_path_bf16():
+    B, H, T, w, g = 1, 2, 1024, 4, 4
+    rp, ci = P.global_csr(B, H, T, g, w)
+    q, k, v = P.make_qkv(B, H, T, seed=43, dtype=torch.bfloat16)
+    print("case window bf16", flush=True)
+    o, lse = run_gpu_window(q, k, v, w, g)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo, rtol=BF16_RTOL)
+    assert_close(lse, ol, what="LSE")
+    o_csr, lse_csr = run_gpu(q, k, v, rp, ci)
+    assert np.array_equal(o, o_csr) and np.array_equal(lse, lse_csr)

@@ -61,6 +61,27 @@ def test_argument_errors_are_reported_before_any_launch(over, code):
     assert _native.last_error()
 
 
+def _fwd_window(**over):
+    args = dict(q=1, k=1, v=1, window=8, g=0, sl=None, o=1, lse=None, B=1, H=1, T=128, D=128,
+                dtype=0, stream=None)
+    args.update(over)
+    lib = _native.load()
+    p = lambda x: None if x is None else ctypes.c_void_p(x)  # noqa: E731
+    return lib.usagi_bsa_fwd_window(p(args["q"]), p(args["k"]), p(args["v"]), args["window"],
+                                    args["g"], p(args["sl"]), p(args["o"]), p(args["lse"]),
+                                    args["B"], args["H"], args["T"], args["D"], args["dtype"],
+                                    p(args["stream"]))
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), -1), (dict(o=None), -1), (dict(window=0), -1), (dict(g=-1), -1),
+    (dict(dtype=7), -2), (dict(D=64), -3), (dict(T=100), -4), (dict(B=0), -1),
+])
+def test_window_argument_errors_are_reported_before_any_launch(over, code):
+    assert _fwd_window(**over) == code
+    assert _native.last_error()
+
+
 def test_shim_rejects_host_tensors_and_bad_shapes():
     q = torch.zeros(1, 1, 128, 128, dtype=torch.float16)
     rp = torch.tensor([[[0, 1]]], dtype=torch.int32)
@@ -71,6 +92,8 @@ def test_shim_rejects_host_tensors_and_bad_shapes():
         usagi_amd.block_sparse_attn_fwd(q.float(), q.float(), q.float(), rp, ci, None)
     with pytest.raises(TypeError):
         usagi_amd.block_sparse_attn_fwd(q.numpy(), q, q, rp, ci, None)
+    with pytest.raises(ValueError, match="GPU"):
+        usagi_amd.block_sparse_attn_fwd_window(q, q, q, 8)
 
 
 def test_setup_on_cpu_device_returns_none_like_the_reference():

@@ -37,6 +37,28 @@ def test_family_rows():
     assert P.retrieval_row(40, 14, 1234, 0, 0) != P.retrieval_row(40, 14, 1234, 0, 1)
 
 
+def analytic_row(i, w, g):
+    """The analytic rows of the window path, as the kernel walks them: the global blocks below
+    the window (min(g, lo) of them), then the window lo .. i (lo = max(0, i - w + 1))."""
+    lo = max(0, i - w + 1)
+    return list(range(min(g, lo))) + list(range(lo, i + 1))
+
+
+def test_analytic_rows_equal_the_csr_rows():
+    # min(g, lo) rather than min(g, i + 1): global blocks inside the window are not repeated
+    for w in (1, 2, 3, 4, 8, 100):
+        for g in (0, 1, 2, 4, 100):
+            for i in range(0, 70):
+                assert analytic_row(i, w, g) == P.global_row(i, g, w), (i, w, g)
+    wl = P.workloads()
+    for name in ("sliding", "global"):
+        ex = wl[name].extra
+        rp, ci = wl[name].csr()
+        for qb in range(wl[name].nqb):
+            row = list(ci[0, 0, rp[0, 0, qb]:rp[0, 0, qb + 1]])
+            assert row == analytic_row(qb, ex["window"], ex["n_global"])
+
+
 def test_mixed_heads():
     rp, ci = P.workloads()["mixed"].csr()
     per_head = [int(rp[0, h, -1]) for h in range(16)]

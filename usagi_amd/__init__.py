@@ -1,7 +1,9 @@
 """usagi_amd — MI355X (gfx950) block-sparse causal attention forward.
 
 The reference's submission-module names are re-exported here:
-VARIANT_MANIFEST, setup, block_sparse_attn_fwd (kernels/v7_blockptr_warpspec.py:24, 201, 251).
+VARIANT_MANIFEST, setup, block_sparse_attn_fwd (kernels/v7_blockptr_warpspec.py:24, 201, 251),
+plus block_sparse_attn_fwd_window, the analytic window / window + global-prefix path
+(kernels/v1_baseline.py:141-322).
 """
 
 from .submission import (  # noqa: F401
@@ -9,6 +11,7 @@ from .submission import (  # noqa: F401
     HEAD_DIM,
     VARIANT_MANIFEST,
     block_sparse_attn_fwd,
+    block_sparse_attn_fwd_window,
     setup,
 )
 

@@ -18,6 +18,7 @@ BF16 = 1
 
 EXPORTED_SYMBOLS = (
     "usagi_bsa_fwd",
+    "usagi_bsa_fwd_window",
     "usagi_bsa_check_csr",
     "usagi_bsa_version",
     "usagi_bsa_last_error",
@@ -47,6 +48,8 @@ def load() -> ctypes.CDLL:
     i32 = ctypes.c_int32
     lib.usagi_bsa_fwd.argtypes = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, p]
     lib.usagi_bsa_fwd.restype = ctypes.c_int
+    lib.usagi_bsa_fwd_window.argtypes = [p, p, p, i32, i32, p, p, p, i32, i32, i32, i32, i32, p]
+    lib.usagi_bsa_fwd_window.restype = ctypes.c_int
     lib.usagi_bsa_check_csr.argtypes = [p, p, i32, i32, i32, i32]
     lib.usagi_bsa_check_csr.restype = ctypes.c_int
     lib.usagi_bsa_version.argtypes = []
@@ -75,6 +78,13 @@ def fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr, out_ptr, ls
     check(load().usagi_bsa_fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr,
                                out_ptr, lse_ptr, batch, heads, seq_len, head_dim, max_nnz,
                                dtype, stream))
+
+
+def fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr, out_ptr, lse_ptr,
+               batch, heads, seq_len, head_dim, dtype, stream) -> None:
+    check(load().usagi_bsa_fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr,
+                                      out_ptr, lse_ptr, batch, heads, seq_len, head_dim, dtype,
+                                      stream))
 
 
 def check_csr_host(row_ptr, col_idx, batch: int, heads: int, nqb: int, max_nnz: int) -> None:

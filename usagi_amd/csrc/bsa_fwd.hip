@@ -77,6 +77,8 @@ struct Args {
   int max_nnz;
   float qk_scale;  // log2(e) / sqrt(128)
   int head_major;  // work-item order, see item_coords
+  int window;      // analytic rows (bsa_fwd_dma_kernel<*, true>): window length in blocks
+  int n_global;    // analytic rows: global prefix blocks
 };
 
 // Work item (workgroup index) -> (query block, b*h).
@@ -443,7 +445,10 @@ __device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
 #define USAGI_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define USAGI_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-template <bool kBf16>
+// kWindow: analytic rows instead of the CSR (no row_ptr / col_idx reads): query block qb attends
+// the global prefix 0 .. n_global-1 and the window max(0, qb-window+1) .. qb, deduplicated and
+// ascending, the rows of kernels/v1_baseline.py:141-322 (_fwd_window, _fwd_window_global).
+template <bool kBf16, bool kWindow>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bsa_fwd_dma_kernel(Args a) {
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kBlk * kHd];  // K[key][d], swizzled
@@ -509,28 +514,45 @@ void bsa_fwd_dma_kernel(Args a) {
     for (int s = 0; s < 8; ++s) qf[s] = *(const u32x4*)(qp + 16 * s);
   }
 
-  const int32_t* rp = a.row_ptr + (size_t)bh * (a.nqb + 1) + qb;
-  int rs = rp[0];
-  int re = rp[1];
-  rs = min(max(rs, 0), a.max_nnz);
-  re = min(max(re, rs), a.max_nnz);
-  const int n_off = max(re - rs - 1, 0);
-  const int32_t* cols = a.col_idx + (size_t)bh * a.max_nnz + rs;
   const int nqb_m1 = a.nqb - 1;
-  // Column indices are held 64 at a time in one VGPR (lane i: entry 64c + i) and picked with
-  // v_readlane, so no vector load sits inside the loop behind the in-flight tile DMAs. Rows
-  // longer than 64 blocks reload the next chunk when they reach it.
+  int n_off = 0;
+  // CSR rows: column indices are held 64 at a time in one VGPR (lane i: entry 64c + i) and
+  // picked with v_readlane, so no vector load sits inside the loop behind the in-flight tile
+  // DMAs. Rows longer than 64 blocks reload the next chunk when they reach it.
+  const int32_t* cols = nullptr;
   int col_chunk = 0;
-  int colv = lane < n_off ? cols[lane] : 0;
+  int colv = 0;
+  // Analytic rows: entries 0 .. win_ng-1 are the global blocks below the window, then the
+  // window from win_lo up to qb - 1.
+  int win_lo = 0;
+  int win_ng = 0;
+  if constexpr (kWindow) {
+    win_lo = max(qb - a.window + 1, 0);
+    win_ng = min(a.n_global, win_lo);
+    n_off = win_ng + (qb - win_lo);
+  } else {
+    const int32_t* rp = a.row_ptr + (size_t)bh * (a.nqb + 1) + qb;
+    int rs = rp[0];
+    int re = rp[1];
+    rs = min(max(rs, 0), a.max_nnz);
+    re = min(max(re, rs), a.max_nnz);
+    n_off = max(re - rs - 1, 0);
+    cols = a.col_idx + (size_t)bh * a.max_nnz + rs;
+    colv = lane < n_off ? cols[lane] : 0;
+  }
   auto key_block = [&](int j) -> int {
-    const int c = j >> 6;
-    if (c != col_chunk) {
-      col_chunk = c;
-      const int e = c * 64 + lane;
-      colv = e < n_off ? cols[e] : 0;
+    if constexpr (kWindow) {
+      return j < win_ng ? j : win_lo + (j - win_ng);
+    } else {
+      const int c = j >> 6;
+      if (c != col_chunk) {
+        col_chunk = c;
+        const int e = c * 64 + lane;
+        colv = e < n_off ? cols[e] : 0;
+      }
+      const int kb = __builtin_amdgcn_readlane(colv, j & 63);
+      return min(max(kb, 0), nqb_m1);
     }
-    const int kb = __builtin_amdgcn_readlane(colv, j & 63);
-    return min(max(kb, 0), nqb_m1);
   };
 
   // Piece i (0..7) of this wave's 8 KiB share of a tile: one 1 KiB DMA. The pieces are spread
@@ -1383,63 +1405,112 @@ extern "C" const char* usagi_bsa_version(void) { return "usagi_bsa 0.1.0 gfx950"
 
 extern "C" const char* usagi_bsa_last_error(void) { return g_err; }
 
-extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
-                             const int32_t* row_ptr, const int32_t* col_idx,
-                             const int32_t* seq_lens, void* out, float* lse, int32_t batch,
-                             int32_t heads, int32_t seq_len, int32_t head_dim, int32_t max_nnz,
-                             int32_t dtype, void* stream) {
-  g_err[0] = '\0';
-  if (!q || !k || !v || !row_ptr || !out) return fail(USAGI_BSA_EINVAL, "null tensor pointer");
+namespace {
+
+// Checks shared by both forward entry points; fills the fields of `a` they have in common.
+int prepare(Args& a, const void* q, const void* k, const void* v, const int32_t* seq_lens,
+            void* out, float* lse, int32_t batch, int32_t heads, int32_t seq_len,
+            int32_t head_dim, int32_t dtype) {
+  if (!q || !k || !v || !out) return fail(USAGI_BSA_EINVAL, "null tensor pointer");
   if (dtype != USAGI_BSA_FP16 && dtype != USAGI_BSA_BF16)
     return fail(USAGI_BSA_EDTYPE, "unknown dtype code %d", (int)dtype);
   if (head_dim != kHd) return fail(USAGI_BSA_EHEADDIM, "head_dim must be %d, got %d", kHd, (int)head_dim);
   if (seq_len <= 0 || seq_len % kBlk != 0)
     return fail(USAGI_BSA_ESEQ, "T must be a positive multiple of %d, got %d", kBlk, (int)seq_len);
   if (batch <= 0 || heads <= 0) return fail(USAGI_BSA_EINVAL, "batch and heads must be positive");
-  if (max_nnz < 0 || (max_nnz > 0 && !col_idx))
-    return fail(USAGI_BSA_EINVAL, "max_nnz must be >= 0 and col_idx non-null when max_nnz > 0");
   const long long bh = (long long)batch * heads;
   const long long nqb = seq_len / kBlk;
   if (bh * nqb > 0x7fffffffLL || bh > 0x7fffffffLL / ((long long)seq_len * kHd) ||
-      bh * (nqb + 1) > 0x7fffffffLL || bh * (long long)max_nnz > 0x7fffffffLL * 4LL)
+      bh * (nqb + 1) > 0x7fffffffLL)
     return fail(USAGI_BSA_EINVAL, "problem too large");
-
-  Args a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
   a.o = static_cast<uint16_t*>(out);
   a.lse = lse;
-  a.row_ptr = row_ptr;
-  a.col_idx = col_idx;
+  a.row_ptr = nullptr;
+  a.col_idx = nullptr;
   a.seq_lens = seq_lens;
   a.heads = heads;
   a.T = seq_len;
   a.nqb = (int)nqb;
   a.bh_count = (int)bh;
-  a.max_nnz = max_nnz;
+  a.max_nnz = 0;
   a.qk_scale = (float)(1.4426950408889634 / sqrt((double)kHd));
   a.head_major = (bh % 8 == 0 && item_order() != 0) ? 1 : 0;
+  a.window = 0;
+  a.n_global = 0;
+  return USAGI_BSA_OK;
+}
 
-  const dim3 grid((unsigned)(bh * nqb));
+int launched() {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
+  return USAGI_BSA_OK;
+}
+
+}  // namespace
+
+extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
+                             const int32_t* row_ptr, const int32_t* col_idx,
+                             const int32_t* seq_lens, void* out, float* lse, int32_t batch,
+                             int32_t heads, int32_t seq_len, int32_t head_dim, int32_t max_nnz,
+                             int32_t dtype, void* stream) {
+  g_err[0] = '\0';
+  Args a;
+  const int rc = prepare(a, q, k, v, seq_lens, out, lse, batch, heads, seq_len, head_dim, dtype);
+  if (rc != USAGI_BSA_OK) return rc;
+  if (!row_ptr) return fail(USAGI_BSA_EINVAL, "null tensor pointer");
+  if (max_nnz < 0 || (max_nnz > 0 && !col_idx))
+    return fail(USAGI_BSA_EINVAL, "max_nnz must be >= 0 and col_idx non-null when max_nnz > 0");
+  if ((long long)a.bh_count * (long long)max_nnz > 0x7fffffffLL * 4LL)
+    return fail(USAGI_BSA_EINVAL, "problem too large");
+  a.row_ptr = row_ptr;
+  a.col_idx = col_idx;
+  a.max_nnz = max_nnz;
+
+  const dim3 grid((unsigned)((long long)a.bh_count * a.nqb));
   const dim3 block(kThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == USAGI_BSA_BF16) {
     if (fp16_kernel() == 2) {
       hipLaunchKernelGGL(bsa_fwd_kernel<true>, grid, block, 0, s, a);
     } else {
-      hipLaunchKernelGGL(bsa_fwd_dma_kernel<true>, grid, block, 0, s, a);
+      hipLaunchKernelGGL((bsa_fwd_dma_kernel<true, false>), grid, block, 0, s, a);
     }
   } else if (fp16_kernel() == 2) {
     hipLaunchKernelGGL(bsa_fwd_kernel<false>, grid, block, 0, s, a);
   } else if (fp16_kernel() == 1) {
-    hipLaunchKernelGGL(bsa_fwd_dma_kernel<false>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<false, false>), grid, block, 0, s, a);
   } else {
     hipLaunchKernelGGL(bsa_fwd_split_kernel, grid, block, 0, s, a);
   }
-  const hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
-  return USAGI_BSA_OK;
+  return launched();
+}
+
+extern "C" int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
+                                    int32_t window, int32_t n_global, const int32_t* seq_lens,
+                                    void* out, float* lse, int32_t batch, int32_t heads,
+                                    int32_t seq_len, int32_t head_dim, int32_t dtype,
+                                    void* stream) {
+  g_err[0] = '\0';
+  Args a;
+  const int rc = prepare(a, q, k, v, seq_lens, out, lse, batch, heads, seq_len, head_dim, dtype);
+  if (rc != USAGI_BSA_OK) return rc;
+  if (window < 1) return fail(USAGI_BSA_EINVAL, "window must be >= 1, got %d", (int)window);
+  if (n_global < 0) return fail(USAGI_BSA_EINVAL, "n_global must be >= 0, got %d", (int)n_global);
+  a.window = window;
+  a.n_global = n_global;
+
+  const dim3 grid((unsigned)((long long)a.bh_count * a.nqb));
+  const dim3 block(kThreads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == USAGI_BSA_BF16) {
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<true, true>), grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<false, true>), grid, block, 0, s, a);
+  }
+  return launched();
 }
 
 extern "C" int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx, int32_t batch,

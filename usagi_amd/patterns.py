@@ -179,8 +179,10 @@ def workloads(seed: int = PATTERN_SEED) -> dict[str, Workload]:
     B2 H16 T8192 D128, and the mixed long-context case."""
     return {
         "plumbing": Workload("plumbing", 1, 4, 1024, lambda: sliding_csr(1, 4, 1024, 4), "sliding"),
-        "sliding": Workload("sliding", 2, 16, 8192, lambda: sliding_csr(2, 16, 8192, 8), "sliding"),
-        "global": Workload("global", 2, 16, 8192, lambda: global_csr(2, 16, 8192, 4, 4), "global"),
+        "sliding": Workload("sliding", 2, 16, 8192, lambda: sliding_csr(2, 16, 8192, 8), "sliding",
+                            {"window": 8, "n_global": 0}),
+        "global": Workload("global", 2, 16, 8192, lambda: global_csr(2, 16, 8192, 4, 4), "global",
+                           {"window": 4, "n_global": 4}),
         "retrieval": Workload("retrieval", 2, 16, 8192,
                               lambda: retrieval_csr(2, 16, 8192, 14, seed), "retrieval"),
         "mixed": Workload("mixed", 1, 16, 16384, lambda: mixed_csr(1, 16, 16384, seed), "mixed"),

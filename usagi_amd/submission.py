@@ -110,6 +110,33 @@ def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
     return out, lse
 
 
+def block_sparse_attn_fwd_window(q, k, v, window, n_global=0, seq_lens=None):
+    """Forward pass over an analytic pattern: query block i attends the global prefix
+    0 .. n_global-1 and the window max(0, i-window+1) .. i (the rows of the reference's unused
+    analytic kernels _fwd_window / _fwd_window_global, kernels/v1_baseline.py:141-322), with no
+    CSR. Equal to block_sparse_attn_fwd on the CSR of that pattern; same tensors and returns.
+    """
+    B, H, T, D = _check_inputs(q, k, v)
+    window, n_global = int(window), int(n_global)
+    if window < 1 or n_global < 0:
+        raise ValueError(f"need window >= 1 and n_global >= 0, got {window}, {n_global}")
+    dev = q.device
+    q = q.contiguous()
+    k = k.contiguous()
+    v = v.contiguous()
+    sl = None
+    if seq_lens is not None:
+        sl = _as_int32_device(torch.as_tensor(seq_lens), dev, (B,))
+    out = torch.empty((B, H, T, D), device=dev, dtype=q.dtype)
+    lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _native.fwd_window(q.data_ptr(), k.data_ptr(), v.data_ptr(), window, n_global,
+                           sl.data_ptr() if sl is not None else None, out.data_ptr(),
+                           lse.data_ptr(), B, H, T, D, _DTYPE_CODES[q.dtype], stream)
+    return out, lse
+
+
 def setup(suite_specs, device, variants):
     """Load the ahead-of-time library and run one tiny launch per distinct T.
 
