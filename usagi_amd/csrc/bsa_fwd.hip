@@ -8,16 +8,20 @@
 // over fp32 scores scaled AFTER the dot product (v7:92, v7:96-100); P is rounded to fp16 before
 // P·V (v7:107). O = acc / l and LSE = m·ln2 + ln l (v7:138-148).
 //
-// Two kernels share that structure:
-//   bsa_fwd_dma_kernel      fp16 (the default): K/V tiles DMA'd HBM -> LDS, V read transposed
-//                           out of LDS, two workgroups per CU, diagonal block first (see the
-//                           comment at the kernel).
+// Three kernels share that structure:
+//   bsa_fwd_dma_kernel<bf16, window>  the default for fp16 and bf16: K/V tiles DMA'd HBM -> LDS,
+//                           V read transposed out of LDS, two workgroups per CU, diagonal block
+//                           first, speculative softmax (see the comment at the kernel). With
+//                           window = true the rows are a window (+ global prefix) computed in
+//                           the kernel instead of read from the CSR (usagi_bsa_fwd_window).
 //   bsa_fwd_kernel<bf16>    register-staged K/V (global -> VGPR -> LDS, V transposed and
-//                           converted to fp16 on the way in); used for bf16 inputs and, with
-//                           USAGI_BSA_FP16_KERNEL=staged, for fp16 A/B runs.
+//                           converted to fp16 on the way in); USAGI_BSA_FP16_KERNEL=staged.
+//   bsa_fwd_split_kernel    fp16, one workgroup per CU, each wave 64 rows x 64 keys, K/V
+//                           double-buffered; USAGI_BSA_FP16_KERNEL=split.
 //
 // Common MI355X design points (not a translation of the Triton program):
-//   * One 256-thread workgroup (4 wave64s) per (b*h, qb); each wave owns 32 query rows.
+//   * One 256-thread workgroup (4 wave64s) per (b*h, qb); each wave owns 32 query rows (the
+//     split kernel: 64 rows and half the keys).
 //   * Everything is computed transposed so that one lane owns one query row:
 //       S^T[key][q] = K · Q^T      (MFMA A = K rows from LDS, B = Q fragment in VGPRs)
 //       O^T[d][q]  += V^T · P^T    (MFMA A = V^T rows from LDS, B = P taken straight from the
@@ -25,10 +29,11 @@
 //     With v_mfma_f32_32x32x16_{f16,bf16}, lane l holds query (l % 32); the other 64 keys of
 //     that query sit in lane l ^ 32, so the row max is one v_permlane32_swap and the running
 //     row sum needs no cross-lane work until the epilogue.
-//   * Workgroups are issued longest-row-first (query blocks in descending order, b*h fastest),
-//     which also keeps all query blocks of one (b, h) on one XCD when B*H is a multiple of 8.
-//   * The running max is only moved when it grows by more than 2^8, so the O rescale is
-//     skipped for almost every block while P stays <= 256 (exact in the normalised result).
+//   * Work order (item_coords): longest row first; when B*H is a multiple of 8, head-major per
+//     XCD, so the K/V tiles of the head an XCD is walking stay in its L2.
+//   * The O rescale is skipped for almost every block: the DMA kernel computes P with the
+//     running max as it stands and checks the row sum of P (a sum <= 2^12 proves every P finite
+//     in fp16); the other two move the running max only when it grows by more than 2^8.
 
 #include <hip/hip_runtime.h>
 
