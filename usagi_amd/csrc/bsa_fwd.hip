@@ -386,18 +386,20 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(Args a) {
 
 
 // ---------------------------------------------------------------------------------------------
-// fp16 kernel: K and V tiles go HBM -> LDS by direct DMA (global_load_lds_dwordx4), so no VGPRs
-// stage them; V is read transposed out of LDS with ds_read_b64_tr_b16. That keeps the wave at
-// <= 256 registers, so two workgroups share each CU (2 waves per SIMD): while one workgroup
-// waits at a barrier or runs softmax VALU, the other keeps the matrix core busy.
+// DMA kernel (fp16; bf16 with the V tile turned into fp16 in LDS): K and V tiles go HBM -> LDS by
+// direct DMA (global_load_lds_dwordx4), so no VGPRs stage them; V is read transposed out of LDS
+// with ds_read_b64_tr_b16. That keeps the wave at <= 256 registers, so two workgroups share each
+// CU (2 waves per SIMD): while one workgroup waits at a barrier or runs softmax VALU, the other
+// keeps the matrix core busy.
 //
 // LDS tiles are 128 rows x 256 B, unpadded, with 16-byte chunks XOR-swizzled inside each row
 // (K: chunk ^ (row % 16), V: chunk ^ 4 * (row % 4)) so that both the DMA writes (1 KiB
 // lane-contiguous per wave instruction) and the MFMA operand reads spread over all banks.
 //
 // Per key block j (two barriers, tiles single-buffered per workgroup, 64 KiB of LDS):
-//   wait K(j) | barrier | S^T = K·Q^T, DMA of V(j) spread between the MFMAs | max, rescale
-//   wait V(j) | barrier | exp2 / fp16 P, O^T += V^T·P^T, DMA of K(j+1) spread between the MFMAs
+//   wait K(j) | barrier | S^T = K·Q^T, DMA of V(j) spread between the MFMAs | P = exp2 in fp16
+//   and its row sum (diagonal: exact row max first; otherwise the running max, checked by the sum)
+//   wait V(j) | barrier | O^T += V^T·P^T, DMA of K(j+1) spread between the MFMAs
 // The diagonal block goes first, so its K tile is requested at entry without reading col_idx.
 // O leaves through LDS as whole rows.
 // A 16-byte-per-lane LDS DMA holds the issuing wave for tens of cycles, so the eight 1 KiB
