@@ -379,3 +379,40 @@ def test_window_path_bf16():
     assert_close(lse, ol, what="LSE")
     o_csr, lse_csr = run_gpu(q, k, v, rp, ci)
     assert np.array_equal(o, o_csr) and np.array_equal(lse, lse_csr)
+
+
+# ------------------------------------------------------------------------------ randomised cases
+
+
+def _random_case(seed):
+    rng = np.random.default_rng(5000 + seed)
+    density = float(rng.uniform(0.05, 0.95))
+    if seed % 6 == 5:
+        B, H, T = 1, 1, 16384  # rows of more than 64 blocks: the column-chunk reload path
+        density = max(density, 0.6)
+    else:
+        B, H = int(rng.choice([1, 2, 3])), int(rng.choice([1, 3, 5, 8]))
+        T = 128 * int(rng.integers(1, 25))
+    dtype = torch.bfloat16 if seed % 3 == 0 else torch.float16
+    seq_lens = None
+    if seed % 2 == 1:
+        seq_lens = [int(x) for x in rng.integers(0, T + 1, size=B)]
+        seq_lens[0] = T  # keep at least one full sequence
+    return B, H, T, density, dtype, seq_lens
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_randomised_shapes_patterns_and_dtypes(seed):
+    """Seeded random B, H (B*H not a multiple of 8 takes the row-major work order), T, CSR
+    density, seq_lens and dtype against the dense oracle."""
+    B, H, T, density, dtype, seq_lens = _random_case(seed)
+    rp, ci = P.random_csr(B, H, T, density, seed)
+    q, k, v = P.make_qkv(B, H, T, seed=100 + seed, dtype=dtype)
+    print(f"case random seed={seed} B{B} H{H} T{T} density={density:.2f} {dtype} "
+          f"seq_lens={seq_lens} max_row={int(np.diff(rp, axis=-1).max())}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci, seq_lens)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci,
+                                     None if seq_lens is None else np.array(seq_lens))
+    rtol = BF16_RTOL if dtype == torch.bfloat16 else 2e-3
+    assert_close(o, oo, rtol=rtol)
+    assert_close(lse, ol, what="LSE")
