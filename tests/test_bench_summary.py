@@ -95,3 +95,10 @@ def test_derived_figures_against_closed_forms(tmp_path):
         assert _field(text, "derived", fam, "mfma_busy") == pytest.approx(0.5)
         assert _field(text, "derived", fam, "lds_bank_conflict_rate") == pytest.approx(0.01)
         assert _field(text, "derived", fam, "hbm_gbs") == pytest.approx(250000 * 1024 / 100e3, rel=1e-3)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    out = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 2
+    assert "one GPU" in out.stderr and not out.stdout.strip()
