@@ -651,12 +651,20 @@ void bsa_fwd_dma_kernel(Args a) {
 
     // ---- masks (v7:94, v7:119-122), row max, lazy rescale
     if constexpr (kDiag) {
+      // Key tiles below the wave's own (t < wave) are visible to all its rows, its own tile
+      // (t == wave) takes the causal mask, and the tiles above (t > wave) were skipped by the
+      // MFMAs: their softmax is skipped too (P·V never reads them).
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        if (t == wave) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = 32 * t + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (key > q_local || !qvalid) st[t][r] = -INFINITY;
+          for (int r = 0; r < 16; ++r) {
+            const int key = 32 * t + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (key > q_local || !qvalid) st[t][r] = -INFINITY;
+          }
+        } else if (t < wave && !qvalid) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
         }
       }
     } else if constexpr (kMaskQ) {
@@ -681,6 +689,7 @@ void bsa_fwd_dma_kernel(Args a) {
       const float neg_m = -m_used;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
+        if (kDiag && (s >> 1) > wave) continue;  // a key tile above the wave's rows
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           pb[s][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(st[s >> 1][8 * (s & 1) + e], scale, neg_m));
@@ -689,6 +698,7 @@ void bsa_fwd_dma_kernel(Args a) {
       float acc = 0.0f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
+        if (kDiag && (s >> 1) > wave) continue;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const half2 pp = {pb[s][2 * e], pb[s][2 * e + 1]};
@@ -701,6 +711,7 @@ void bsa_fwd_dma_kernel(Args a) {
       float mx = st[0][0];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
+        if (kDiag && t > wave) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
       }
