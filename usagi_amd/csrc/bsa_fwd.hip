@@ -728,8 +728,9 @@ void bsa_fwd_dma_kernel(Args a) {
       }
     };
     if constexpr (kDiag) {
-      const float m_new = fmaxf(m_used, row_max() * scale);
-      if (__any(m_new > m_used)) rescale(m_new);
+      // The diagonal block is the item's first: O and l are still zero, so the row max is taken
+      // without a rescale.
+      m_used = fmaxf(m_used, row_max() * scale);
       make_p();
     } else {
       make_p();
