@@ -1,13 +1,13 @@
 """CPU oracle of the block-sparse causal attention forward — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module, and only
-as the checker (or the timed CPU baseline); the product path (usagi_amd) never imports it.
+to check results (or as the timed CPU baseline); the product path (usagi_amd) never imports it.
 
 Two restatements of the reference's math:
 
   dense_masked()  fp32 (or fp64) softmax attention over the dense token mask
                   block_mask(CSR) ∧ causal ∧ key < seq_len, rows t >= seq_len -> O = 0,
-                  LSE = -inf. This is the north-star oracle; for a valid CSR (ascending,
+                  LSE = -inf. This is the parity reference; for a valid CSR (ascending,
                   diagonal last, all kb <= qb) it equals the reference's walk
                   (kernels/v7_blockptr_warpspec.py:83-148).
   blockwise_v7()  the reference's own algorithm, step for step: per (b*h, qb) an online exp2

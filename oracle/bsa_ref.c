@@ -1,7 +1,7 @@
 /*
  * bsa_ref.c — plain-C restatement of the reference's CSR block-sparse causal attention walk.
  * TEST INFRASTRUCTURE ONLY: built by oracle/build.py into oracle/_build/ and loaded by tests/
- * and by bench.py's cpu_baseline leg as the checker / timed CPU port. The product library
+ * and by bench.py's cpu_baseline leg to check results / as the timed CPU port. The product library
  * (usagi_amd/lib/libusagi_bsa.so) never links or calls it.
  *
  * Follows the Triton program _fwd_csr of kernels/v7_blockptr_warpspec.py:45-148 step for step,
