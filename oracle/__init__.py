@@ -1,7 +1,7 @@
 """CPU oracle of the block-sparse causal attention forward — TEST INFRASTRUCTURE ONLY.
 
-Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
-checker or the timed CPU port; never by the usagi_amd package.
+Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, to check
+results or as the timed CPU port; never by the usagi_amd package.
 
   bsa_oracle.dense_masked   numpy fp32/fp64 dense-masked softmax attention (math oracle)
   bsa_oracle.blockwise_v7   numpy restatement of the reference CSR walk
