@@ -72,7 +72,8 @@ int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
                          int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
                          int32_t dtype, void* stream);
 
-/* Host-side CSR validator over HOST copies of row_ptr / col_idx. It checks the preconditions
+/* Host-side CSR validator over HOST copies of row_ptr / col_idx; no counterpart in the reference,
+ * which does not validate its input (kernels/v7_blockptr_warpspec.py:155-191). It checks the preconditions
  * under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-111 equals
  * block-mask ∧ causal attention: row_ptr[0] == 0, monotone, row_ptr[nqb] <= max_nnz, every row
  * non-empty, strictly ascending, every entry in [0, qb], and the last entry == qb.
@@ -80,10 +81,13 @@ int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
 int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
                         int32_t batch, int32_t heads, int32_t num_q_blocks, int32_t max_nnz);
 
-/* Version string of this library, e.g. "usagi_bsa 0.1.0 gfx950". */
+/* Version string of this library, e.g. "usagi_bsa 0.1.0 gfx950". No counterpart in the
+ * reference (its module has no version). */
 const char* usagi_bsa_version(void);
 
-/* Message for the calling thread's most recent nonzero return ("" if none). */
+/* Message for the calling thread's most recent nonzero return ("" if none). Stands in for the
+ * reference's exceptions: the RuntimeError carrying the driver's code at
+ * kernels/v1_baseline.py:126-128 (the Triton versions raise from the JIT launch). */
 const char* usagi_bsa_last_error(void);
 
 #ifdef __cplusplus
