@@ -410,6 +410,29 @@ def main() -> int:
         analytic[name] = {"window": ex["window"], "n_global": ex["n_global"],
                           "median_ms": round(mw, 4), "csr_median_ms": round(mc, 4),
                           "ratio_to_csr": round(mw / mc, 4)}
+    # The long-context mixed workload (B1 H16 T16384, rows of 1-26 blocks varying by head): a
+    # parity configuration, timed here for information only (not part of the geomean).
+    others = {}
+    mw = wl["mixed"]
+    mq, mk, mv = (x.to(dev) for x in P.make_qkv(mw.B, mw.H, mw.T, seed=args.seed))
+    mrp, mci = mw.csr()
+    mrpd, mcid = torch.from_numpy(mrp).to(dev), torch.from_numpy(mci).to(dev)
+    for _ in range(5):
+        block_sparse_attn_fwd(mq, mk, mv, mrpd, mcid, None)
+    ev_m = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(args.steps)]
+    for a, b in ev_m:
+        a.record(stream)
+        block_sparse_attn_fwd(mq, mk, mv, mrpd, mcid, None)
+        b.record(stream)
+    torch.cuda.synchronize()
+    mmed = float(np.median([a.elapsed_time(b) for a, b in ev_m]))
+    mfl = P.active_blocks(mrp) * FLOP_PER_BLOCK
+    others["mixed"] = {"B": mw.B, "H": mw.H, "T": mw.T, "active_blocks": P.active_blocks(mrp),
+                      "median_ms": round(mmed, 4), "tflops": round(mfl / mmed / 1e9, 1),
+                      "frac_peak": round(mfl / mmed / 1e9 / PEAK_FP16_TFLOPS, 4)}
+    del mq, mk, mv
+
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
     roofline = {
@@ -451,6 +474,7 @@ def main() -> int:
             "latency_timing": "HIP events around each call on the launch stream; median over "
                               "the timed steps per family",
             "analytic_rows": analytic,
+            "other_workloads": others,
             "input_seed": args.seed,
             "pattern_seed": P.PATTERN_SEED,
         },
