@@ -595,8 +595,8 @@ void bsa_fwd_dma_kernel(Args a) {
   float l_part = 0.0f;
   const float scale = a.qk_scale;
 
-  // vmcnt(0): Q, the column chunk and the diagonal K tile have landed. Issued as a real
-  // s_waitcnt so the compiler knows no load of its own is outstanding inside the loop.
+  // vmcnt(0): Q, the column chunk (CSR rows) and the diagonal K tile have landed. Issued as a
+  // real s_waitcnt so the compiler knows no load of its own is outstanding inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // One key block: the diagonal (kDiag, j = -1, causal mask) or off-diagonal entry j.
@@ -624,9 +624,11 @@ void bsa_fwd_dma_kernel(Args a) {
     // V(j) DMA pieces go out between the QK MFMAs (the V buffer is free after the barrier).
     u32x4 kop[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * (0 ^ k_x));
+    for (int t = 0; t < 4; ++t) {
+      if (!kDiag || t <= wave) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * (0 ^ k_x));
+    }
     // On the diagonal, key tile t (keys 32t .. 32t+31) lies above every row of wave w when t > w:
-    // those tiles are skipped (their scores stay 0 and are masked below).
+    // those tiles are skipped here, in the softmax and in P·V.
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
