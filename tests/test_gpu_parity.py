@@ -416,3 +416,33 @@ def test_randomised_shapes_patterns_and_dtypes(seed):
     rtol = BF16_RTOL if dtype == torch.bfloat16 else 2e-3
     assert_close(o, oo, rtol=rtol)
     assert_close(lse, ol, what="LSE")
+
+
+def test_empty_rows_take_the_implicit_diagonal():
+    """max_nnz = 0 (every CSR row empty): like the reference's walk (v7:83-111), each query block
+    still attends its implicit diagonal, so O and LSE equal those of a diagonal-only CSR."""
+    B, H, T = 1, 3, 512
+    nqb = T // 128
+    q, k, v = P.make_qkv(B, H, T, seed=51)
+    rp0 = np.zeros((B, H, nqb + 1), dtype=np.int32)
+    ci0 = np.zeros((B, H, 0), dtype=np.int32)
+    rp1, ci1 = P.sliding_csr(B, H, T, 1)
+    print("case empty rows", flush=True)
+    o0, l0 = run_gpu(q, k, v, rp0, ci0)
+    o1, l1 = run_gpu(q, k, v, rp1, ci1)
+    assert np.array_equal(o0, o1) and np.array_equal(l0, l1)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp1, ci1)
+    assert_close(o0, oo)
+    assert_close(l0, ol, what="LSE")
+
+
+def test_many_heads_single_block():
+    """256 (b, h) pairs at T = 128: one query block each, head-major work order."""
+    B, H, T = 4, 64, 128
+    rp, ci = P.sliding_csr(B, H, T, 1)
+    q, k, v = P.make_qkv(B, H, T, seed=52)
+    print("case many heads", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
