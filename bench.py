@@ -15,7 +15,12 @@ call is bracketed by HIP events on the launch stream; the per-family median give
 The warmup is W steps plus, if needed, more whole steps until S seconds have passed (reported as
 warmup_extra_steps): from idle the GPU takes tens of ms of sustained load to reach steady clocks.
 
-Prints one JSON line.
+Prints one JSON line. Besides the contract fields: per family launch_ms (mean per-call event time
+of the timed steps, the roofline's launch duration) and burst_ms (back-to-back bursts, after the
+timed steps); config.analytic_rows (the analytic window path against the CSR path on the sliding
+and global families); config.other_workloads (the long-context mixed workload, outside the
+geomean); cpu_baseline (PyTorch CPU dense-masked attention on the host, with the C walk beside
+it). --pmc-summary turns rocprofv3 counter runs into per-family traffic and derived figures.
 """
 
 from __future__ import annotations
