@@ -8,19 +8,25 @@ D=128, fp16, plus the fraction of dense fp16 MFMA peak counting only active 128x
 (4·128^3 FLOP each).
 
 A step is one forward call of each family on synthetic inputs already resident in HBM. Every
-call is bracketed by HIP events on the launch stream; the per-family median gives the latency.
+call is bracketed by HIP events on the launch stream. The K timed steps are split into
+--repeats consecutive groups; a family's latency is the median over the groups of its median
+within each group (the reference's protocol of comparing medians over repeated runs,
+docs/OPTIMIZATION_JOURNAL.md:135, 189-190).
 
-    python bench.py [--steps K] [--warmup W] [--min-warmup-s S] [--cpu-heads N | --no-cpu]
+    python bench.py [--steps K] [--warmup W] [--repeats R] [--min-warmup-s S] [--no-cpu]
 
 The warmup is W steps plus, if needed, more whole steps until S seconds have passed (reported as
 warmup_extra_steps): from idle the GPU takes tens of ms of sustained load to reach steady clocks.
 
-Prints one JSON line. Besides the contract fields: per family launch_ms (mean per-call event time
-of the timed steps, the roofline's launch duration) and burst_ms (back-to-back bursts, after the
-timed steps); config.analytic_rows (the analytic window path against the CSR path on the sliding
-and global families); config.other_workloads (the long-context mixed workload, outside the
-geomean); cpu_baseline (PyTorch CPU dense-masked attention on the host, with the C walk beside
-it). --pmc-summary turns rocprofv3 counter runs into per-family traffic and derived figures.
+Prints one JSON line. Besides the contract fields, after the timed steps: per family launch_ms
+(mean per-call event time, the roofline's launch duration) and burst_ms (back-to-back bursts);
+config.full_seq_variant (seq_lens None, the kernel with the length masks compiled out, against
+seq_lens of all T); config.analytic_rows (the analytic window path against the CSR path);
+config.reference_conditions (bf16 inputs, and bf16 with variable seq_lens, as the reference was
+scored); config.other_workloads (the long-context mixed workload, with and without the work
+plan); cpu_baseline (PyTorch CPU dense-masked attention on the host, median of 3, with the C
+walk beside it). profile.family_dispatches counts the kernel dispatches of the warmup and timed
+steps, which --pmc-summary attributes to the families when given the JSON of a profiled run.
 """
 
 from __future__ import annotations
@@ -30,6 +36,7 @@ import json
 import math
 import os
 import re
+import subprocess
 import sys
 import time
 
@@ -40,13 +47,18 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
+from usagi_amd import _native  # noqa: E402
 from usagi_amd import block_sparse_attn_fwd, block_sparse_attn_fwd_window  # noqa: E402
 from usagi_amd import patterns as P  # noqa: E402
 
 METRIC = "geomean fwd ms @B2 H16 T8192 D128 over 3 sparsity families; % fp16 MFMA peak"
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, published
 FLOP_PER_BLOCK = 4 * 128 ** 3
+# MFMAs the kernel issues for a diagonal block: 160 of a full block's 256 (each wave skips the
+# key tiles above its 32 query rows in Q·K^T and the k-steps above them in P·V).
+DIAG_MFMA_SHARE = 160 / 256
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "bsa_fwd_hbm_traffic_b2h16t8192.txt")
+REF_SEQ_LENS = [8192, 5000]  # variable sequence lengths for the reference-condition lines
 
 
 def geomean(xs):
@@ -54,6 +66,13 @@ def geomean(xs):
 
 
 def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -78,24 +97,34 @@ def read_traffic():
     return out or None
 
 
-def cpu_baseline(fams, inputs, n_heads: int, c_heads: int):
+def executed_flop(row_ptr) -> int:
+    """FLOP of the MFMAs the kernel issues: full blocks, and 160/256 of one per diagonal."""
+    n_diag = int(np.prod(row_ptr.shape[:-1])) * (row_ptr.shape[-1] - 1)
+    return int((P.active_blocks(row_ptr) - n_diag * (1 - DIAG_MFMA_SHARE)) * FLOP_PER_BLOCK)
+
+
+def cpu_baseline(fams, inputs, n_heads: int, c_heads: int, runs: int):
     """The reference math as PyTorch CPU fp32 dense-masked attention (oracle/torch_dense.py) on
     the host cores, per family over heads b < B, h < n_heads (all heads by default: the full
-    workload), projected to B2 H16 by head count when fewer heads are run. The C restatement of
-    the reference's blockwise CSR walk (oracle/bsa_ref.c, OpenMP) is timed beside it on c_heads
-    heads and projected by active blocks."""
+    workload), projected to B2 H16 by head count when fewer heads are run; the median of `runs`
+    runs per family. The C restatement of the reference's blockwise CSR walk (oracle/bsa_ref.c,
+    OpenMP) is timed beside it on c_heads heads, once, projected by active blocks."""
     from oracle import c_ref, torch_dense
 
     q, k, v = inputs
     B, H = q.shape[:2]
-    cores = torch.get_num_threads()
+    threads = torch.get_num_threads()
     heads = [(b, h) for b in range(B) for h in range(min(n_heads, H))]
-    per, per_c = {}, {}
+    per, per_c, spread = {}, {}, {}
     for name, (rp, ci) in fams.items():
         rpt, cit = torch.from_numpy(rp), torch.from_numpy(ci)
-        t0 = time.perf_counter()
-        torch_dense.dense_masked(q, k, v, rpt, cit, heads=heads)
-        per[name] = (time.perf_counter() - t0) * 1e3 * (B * H) / len(heads)
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            torch_dense.dense_masked(q, k, v, rpt, cit, heads=heads)
+            ts.append((time.perf_counter() - t0) * 1e3 * (B * H) / len(heads))
+        per[name] = float(np.median(ts))
+        spread[name] = [round(x, 1) for x in ts]
         if c_heads:
             qs, ks, vs = (x[:1, :c_heads].float().numpy() for x in (q, k, v))
             rps, cis = rp[:1, :c_heads], ci[:1, :c_heads]
@@ -108,36 +137,42 @@ def cpu_baseline(fams, inputs, n_heads: int, c_heads: int):
     out = {
         "value": round(geomean(list(per.values())), 3),
         "unit": "ms",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
         "sample": (f"PyTorch CPU fp32 dense-masked attention (oracle/torch_dense.py: block mask "
                    f"from the CSR, causal, query slabs of 1024 rows against keys up to the slab "
-                   f"end) on {sample}; geomean over the 3 families of one run each; host CPU: "
-                   f"{cpu_model()}, {cores} threads"),
+                   f"end) on {sample}; per family the median of {runs} runs, then the geomean "
+                   f"over the 3 families; {threads} threads (the process's thread budget; "
+                   f"os.cpu_count() = {os.cpu_count()}); host CPU: {cpu_model()}"),
         "per_family_ms": {k2: round(v2, 3) for k2, v2 in per.items()},
+        "per_family_runs_ms": spread,
+        "os_cpu_count": os.cpu_count(),
     }
     if per_c:
         out["blockwise_c_port"] = {
             "value": round(geomean(list(per_c.values())), 3),
             "unit": "ms",
             "sample": (f"oracle/bsa_ref.c (the reference's CSR walk in C, fp32, OpenMP) on heads "
-                       f"b=0, h<{c_heads}, projected by active blocks"),
+                       f"b=0, h<{c_heads}, projected by active blocks, one run"),
             "per_family_ms": {k2: round(v2, 3) for k2, v2 in per_c.items()},
         }
     return out
 
 
 KERNEL = "bsa_fwd_dma_kernel"
+CALIB_KERNEL = "neg"
 
 
-def pmc_summary(paths, calib_mib: int) -> int:
+def pmc_summary(paths, calib_mib: int, bench_json: str | None) -> int:
     """Per-family averages of rocprofv3 --pmc counters for the attention kernel.
 
-    Dispatches of the kernel come in family order (sliding, global, retrieval) on every warmup
-    and timed step, so dispatch i belongs to FAMILIES[i % 3]. The calibration kernel is the
-    last dispatch before the first attention dispatch (the elementwise -in of
-    --calib-copy-mib MiB, which reads and writes exactly that many bytes); FETCH_SIZE and
-    WRITE_SIZE (KiB) are each scaled by (known KiB / counter KiB) of that kernel.
+    The first profile.family_dispatches dispatches of the kernel (read from the JSON line the
+    profiled bench run printed, --bench-json) are its warmup and timed steps, issued in family
+    order (sliding, global, retrieval) every step, so dispatch i of them belongs to
+    FAMILIES[i % 3]; later dispatches (bursts, the other lines of the bench) are left out. The
+    calibration kernel is the elementwise negation of --calib-copy-mib MiB (it reads and writes
+    exactly that many bytes); FETCH_SIZE and WRITE_SIZE (KiB) are each scaled by (known KiB /
+    counter KiB) of that kernel.
 
     When a pass also ran with --kernel-trace, its run_kernel_trace.csv (next to the counter
     file) gives each dispatch's duration, and run_agent_info.csv the part's XCD and SIMD
@@ -150,6 +185,12 @@ def pmc_summary(paths, calib_mib: int) -> int:
     if not calib_mib:
         print("--pmc-summary needs the --calib-copy-mib value of the profiled run", file=sys.stderr)
         return 2
+    if not bench_json:
+        print("--pmc-summary needs --bench-json (the JSON line of the profiled run)", file=sys.stderr)
+        return 2
+    with open(bench_json) as f:
+        line = [x for x in f.read().splitlines() if x.startswith("{")][-1]
+    n_fam = int(json.loads(line)["profile"]["family_dispatches"])
     known_kib = calib_mib * 1024.0
     sums: dict = {}
     durs: dict = {}
@@ -178,19 +219,19 @@ def pmc_summary(paths, calib_mib: int) -> int:
                     if r.get("Name", "").startswith("gfx"):
                         n_xcc, n_simd = int(r["Num_Xcc"]), int(r["Simd_Count"])
         order = sorted(by_disp)
-        first = next(i for i, d in enumerate(order) if KERNEL in by_disp[order[i]]["name"])
-        if first > 0:
-            cal = by_disp[order[first - 1]]
-            calib_name = cal["name"]
-            calib.update(cal["ctr"])
-        i = 0
-        for d in order[first:]:
-            e = by_disp[d]
-            if KERNEL not in e["name"]:
-                continue
+        cal = [d for d in order if CALIB_KERNEL in by_disp[d]["name"]
+               and KERNEL not in by_disp[d]["name"]]
+        if cal:
+            calib_name = by_disp[cal[0]]["name"]
+            calib.update(by_disp[cal[0]]["ctr"])
+        att = [d for d in order if KERNEL in by_disp[d]["name"]]
+        if len(att) < n_fam:
+            print(f"{path}: {len(att)} kernel dispatches, fewer than the {n_fam} of the warmup and "
+                  f"timed steps", file=sys.stderr)
+            return 2
+        for i, d in enumerate(att[:n_fam]):
             fam = P.FAMILIES[i % len(P.FAMILIES)]
-            i += 1
-            for cname, val in e["ctr"].items():
+            for cname, val in by_disp[d]["ctr"].items():
                 s = sums.setdefault(fam, {}).setdefault(cname, [0.0, 0])
                 s[0] += val
                 s[1] += 1
@@ -198,7 +239,8 @@ def pmc_summary(paths, calib_mib: int) -> int:
                 t = durs.setdefault(fam, [0.0, 0])
                 t[0] += dur_of[d]
                 t[1] += 1
-    print(f"kernel {KERNEL}; calibration kernel: {calib_name}")
+    print(f"kernel {KERNEL}: the first {n_fam} dispatches of each pass (warmup and timed steps); "
+          f"calibration kernel: {calib_name}")
     for cname, val in sorted(calib.items()):
         print(f"calibration {cname} {val:.1f}")
     factor = {}
@@ -225,7 +267,7 @@ def pmc_summary(paths, calib_mib: int) -> int:
         if fam not in durs:
             continue
         dur_ns = durs[fam][0] / durs[fam][1]
-        flop = P.active_blocks(wl[fam].csr()[0]) * 4 * P.BLOCK ** 3
+        flop = P.active_blocks(wl[fam].csr()[0]) * FLOP_PER_BLOCK
         tflops = flop / dur_ns / 1e3
         print(f"derived {fam} duration_us {dur_ns / 1e3:.1f}  (kernel trace of the counter passes, "
               f"{durs[fam][1]} dispatches)  tflops_active {tflops:.1f}")
@@ -251,11 +293,40 @@ def pmc_summary(paths, calib_mib: int) -> int:
     return 0
 
 
+def event_pair():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_calls(fns, n, stream):
+    """n rounds of calling every fn once, each call between its own events; returns the
+    per-call times (ms) per fn."""
+    ev = [[event_pair() for _ in range(n)] for _ in fns]
+    for s in range(n):
+        for i, fn in enumerate(fns):
+            a, b = ev[i][s]
+            a.record(stream)
+            fn()
+            b.record(stream)
+    torch.cuda.synchronize()
+    return [[a.elapsed_time(b) for a, b in e] for e in ev]
+
+
+def warm(fns, seconds):
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            for fn in fns:
+                fn()
+        torch.cuda.synchronize()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=150)
+    ap.add_argument("--repeats", type=int, default=5,
+                    help="groups the timed steps are split into (median of the group medians)")
     ap.add_argument("--burst", type=int, default=10,
                     help="calls per event pair of the back-to-back bursts timed after the timed "
                          "steps (burst_ms, informational)")
@@ -266,9 +337,12 @@ def main() -> int:
                          "and the first calls after idle run up to 20%% slower")
     ap.add_argument("--cpu-heads", type=int, default=16,
                     help="heads per batch entry timed by the CPU baseline (16 = all)")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="CPU baseline runs per family (median)")
     ap.add_argument("--cpu-c-heads", type=int, default=4,
                     help="heads timed by the C blockwise port beside it (0 = skip)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the informational lines after the timed steps")
     ap.add_argument("--seed", type=int, default=P.INPUT_SEED)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the warmup, run one elementwise kernel (out = -in, fp32) that "
@@ -277,10 +351,11 @@ def main() -> int:
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="summarise rocprofv3 --pmc counter_collection.csv files of a run of "
                          "this script (made with --calib-copy-mib) and exit; no GPU is used")
+    ap.add_argument("--bench-json", help="with --pmc-summary: the JSON output of that run")
     args = ap.parse_args()
 
     if args.pmc_summary:
-        return pmc_summary(args.pmc_summary, args.calib_copy_mib)
+        return pmc_summary(args.pmc_summary, args.calib_copy_mib, args.bench_json)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU mode "
@@ -303,6 +378,16 @@ def main() -> int:
         rp, ci = wl[name].csr()
         fams[name] = (rp, ci)
         dev_csr[name] = (torch.from_numpy(rp).to(dev), torch.from_numpy(ci).to(dev))
+    # Everything the lines after the timed steps use is built here, before the GPU warms up.
+    mw = wl["mixed"]
+    mixed = None
+    if not args.no_extra:
+        mq, mk, mv = (x.to(dev) for x in P.make_qkv(mw.B, mw.H, mw.T, seed=args.seed))
+        mrp, mci = mw.csr()
+        mixed = (mq, mk, mv, mrp, torch.from_numpy(mrp).to(dev), torch.from_numpy(mci).to(dev))
+        qb16, kb16, vb16 = (x.to(torch.bfloat16) for x in (q, k, v))
+    full_sl = torch.full((B,), T, dtype=torch.int32, device=dev)
+    ref_sl = torch.tensor(REF_SEQ_LENS, dtype=torch.int32, device=dev)
 
     if args.calib_copy_mib:
         n = args.calib_copy_mib * (1 << 20) // 4
@@ -313,26 +398,26 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    def call(name):
+    def call(name, qq=q, kk=k, vv=v, sl=None):
         rp, ci = dev_csr[name]
-        return block_sparse_attn_fwd(q, k, v, rp, ci, None)
+        return block_sparse_attn_fwd(qq, kk, vv, rp, ci, sl)
 
+    step_fns = [(lambda n=name: call(n)) for name in P.FAMILIES]
     for _ in range(args.warmup):
-        for name in P.FAMILIES:
-            call(name)
+        for fn in step_fns:
+            fn()
     torch.cuda.synchronize()
     extra = 0
     t_w = time.perf_counter()
     while time.perf_counter() - t_w < args.min_warmup_s and args.min_warmup_s > 0:
         for _ in range(10):
-            for name in P.FAMILIES:
-                call(name)
+            for fn in step_fns:
+                fn()
             extra += 1
         torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream(dev)
-    ev = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)] for n in P.FAMILIES}
+    ev = {n: [event_pair() for _ in range(args.steps)] for n in P.FAMILIES}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
@@ -344,99 +429,119 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
+    groups = max(1, min(args.repeats, args.steps))
+    bounds = np.linspace(0, args.steps, groups + 1).astype(int)
     fam_out = {}
-    medians, means, flops = [], [], []
+    medians, flops, exec_flops = [], [], []
+    launch_ms = {}
     for name in P.FAMILIES:
-        ts = [a.elapsed_time(b) for a, b in ev[name]]
-        med = float(np.median(ts))
-        mean = float(np.mean(ts))
+        ts = np.array([a.elapsed_time(b) for a, b in ev[name]])
+        group_meds = [float(np.median(ts[bounds[g]:bounds[g + 1]])) for g in range(groups)]
+        med = float(np.median(group_meds))
         fl = P.active_blocks(fams[name][0]) * FLOP_PER_BLOCK
+        efl = executed_flop(fams[name][0])
         medians.append(med)
-        means.append(mean)
         flops.append(fl)
+        exec_flops.append(efl)
+        launch_ms[name] = float(np.mean(ts))
         fam_out[name] = {
             "median_ms": round(med, 4),
-            "mean_ms": round(mean, 4),
+            "group_medians_ms": [round(x, 4) for x in group_meds],
+            "median_all_steps_ms": round(float(np.median(ts)), 4),
+            "mean_ms": round(float(np.mean(ts)), 4),
+            "launch_ms": round(launch_ms[name], 4),
             "active_blocks": P.active_blocks(fams[name][0]),
             "tflops": round(fl / med / 1e9, 1),
             "frac_peak": round(fl / med / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "executed_mfma_tflops": round(efl / med / 1e9, 1),
         }
-
     value = geomean(medians)
-
-    # Kernel launch duration for the roofline: the mean per-call event time of the timed steps,
-    # per family, on the launch stream. It includes each call's event packets and dispatch gap
-    # (a few us over the kernel's own duration), so it is, if anything, long. Back-to-back bursts
-    # of --burst calls are timed after the timed region too (burst_ms, per call): sustained load
-    # without gaps lowers the clock, so they run a few percent slower still.
-    launch_ms = {}
-    for name in P.FAMILIES:
-        launch_ms[name] = float(np.mean([a.elapsed_time(b) for a, b in ev[name]]))
-        fam_out[name]["launch_ms"] = round(launch_ms[name], 4)
     mean_launch = sum(launch_ms.values()) / len(launch_ms)
-    burst = {n: [] for n in P.FAMILIES}
-    for _ in range(args.burst_reps):
-        for name in P.FAMILIES:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(args.burst):
-                call(name)
-            b.record(stream)
-            burst[name].append((a, b))
-    torch.cuda.synchronize()
-    for name in P.FAMILIES:
-        fam_out[name]["burst_ms"] = round(
-            float(np.mean([a.elapsed_time(b) / args.burst for a, b in burst[name]])), 4)
 
-    # Analytic rows (no CSR, block_sparse_attn_fwd_window) for the families that are a window or
-    # a window plus a global prefix, call by call against the CSR path for a like-for-like ratio.
-    analytic = {}
-    for name in P.FAMILIES:
-        ex = wl[name].extra
-        if "window" not in ex:
-            continue
-        ev_w = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                for _ in range(args.steps)]
-        ev_c = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                for _ in range(args.steps)]
-        for s in range(args.steps):
-            a, b = ev_w[s]
-            a.record(stream)
-            block_sparse_attn_fwd_window(q, k, v, ex["window"], ex["n_global"])
-            b.record(stream)
-            a, b = ev_c[s]
-            a.record(stream)
-            call(name)
-            b.record(stream)
+    extra_cfg = {}
+    if not args.no_extra:
+        # Back-to-back bursts: sustained load without gaps lowers the clock a little further.
+        burst = {n: [] for n in P.FAMILIES}
+        for _ in range(args.burst_reps):
+            for name in P.FAMILIES:
+                a, b = event_pair()
+                a.record(stream)
+                for _ in range(args.burst):
+                    call(name)
+                b.record(stream)
+                burst[name].append((a, b))
         torch.cuda.synchronize()
-        mw = float(np.median([a.elapsed_time(b) for a, b in ev_w]))
-        mc = float(np.median([a.elapsed_time(b) for a, b in ev_c]))
-        analytic[name] = {"window": ex["window"], "n_global": ex["n_global"],
-                          "median_ms": round(mw, 4), "csr_median_ms": round(mc, 4),
-                          "ratio_to_csr": round(mw / mc, 4)}
-    # The long-context mixed workload (B1 H16 T16384, rows of 1-26 blocks varying by head): a
-    # parity configuration, timed here for information only (not part of the geomean).
-    others = {}
-    mw = wl["mixed"]
-    mq, mk, mv = (x.to(dev) for x in P.make_qkv(mw.B, mw.H, mw.T, seed=args.seed))
-    mrp, mci = mw.csr()
-    mrpd, mcid = torch.from_numpy(mrp).to(dev), torch.from_numpy(mci).to(dev)
-    for _ in range(5):
-        block_sparse_attn_fwd(mq, mk, mv, mrpd, mcid, None)
-    ev_m = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(args.steps)]
-    for a, b in ev_m:
-        a.record(stream)
-        block_sparse_attn_fwd(mq, mk, mv, mrpd, mcid, None)
-        b.record(stream)
-    torch.cuda.synchronize()
-    mmed = float(np.median([a.elapsed_time(b) for a, b in ev_m]))
-    mfl = P.active_blocks(mrp) * FLOP_PER_BLOCK
-    others["mixed"] = {"B": mw.B, "H": mw.H, "T": mw.T, "active_blocks": P.active_blocks(mrp),
-                      "median_ms": round(mmed, 4), "tflops": round(mfl / mmed / 1e9, 1),
-                      "frac_peak": round(mfl / mmed / 1e9 / PEAK_FP16_TFLOPS, 4)}
-    del mq, mk, mv
+        for name in P.FAMILIES:
+            fam_out[name]["burst_ms"] = round(
+                float(np.mean([a.elapsed_time(b) / args.burst for a, b in burst[name]])), 4)
+
+        # seq_lens None runs the variant with every length mask compiled out; seq_lens of all T
+        # runs the masked one on the same work. Call by call, alternating.
+        full_seq = {}
+        for name in P.FAMILIES:
+            t_none, t_full = time_calls([lambda n=name: call(n),
+                                         lambda n=name: call(n, sl=full_sl)], args.steps, stream)
+            mn, mf = float(np.median(t_none)), float(np.median(t_full))
+            full_seq[name] = {"seq_lens_none_ms": round(mn, 4), "seq_lens_all_T_ms": round(mf, 4),
+                              "ratio_none_to_all_T": round(mn / mf, 4)}
+        extra_cfg["full_seq_variant"] = full_seq
+
+        # Analytic rows (no CSR, block_sparse_attn_fwd_window) for the window-shaped families.
+        analytic = {}
+        for name in P.FAMILIES:
+            ex = wl[name].extra
+            if "window" not in ex:
+                continue
+            t_w, t_c = time_calls([
+                lambda ex=ex: block_sparse_attn_fwd_window(q, k, v, ex["window"], ex["n_global"]),
+                lambda n=name: call(n)], args.steps, stream)
+            mw_, mc = float(np.median(t_w)), float(np.median(t_c))
+            analytic[name] = {"window": ex["window"], "n_global": ex["n_global"],
+                              "median_ms": round(mw_, 4), "csr_median_ms": round(mc, 4),
+                              "ratio_to_csr": round(mw_ / mc, 4)}
+        extra_cfg["analytic_rows"] = analytic
+
+        # The reference was scored on bf16 inputs with variable sequence lengths
+        # (docs/OPTIMIZATION_JOURNAL.md:14-16): the same three families that way.
+        ref = {}
+        for label, sl in (("bf16", None), (f"bf16_seq_lens_{REF_SEQ_LENS[0]}_{REF_SEQ_LENS[1]}", ref_sl)):
+            fns = [(lambda n=name, s=sl: call(n, qb16, kb16, vb16, s)) for name in P.FAMILIES]
+            warm(fns, args.min_warmup_s)
+            ts = time_calls(fns, args.steps, stream)
+            meds = {n: float(np.median(t)) for n, t in zip(P.FAMILIES, ts)}
+            ref[label] = {"median_ms": {n: round(m, 4) for n, m in meds.items()},
+                          "geomean_ms": round(geomean(list(meds.values())), 4)}
+        ref["note"] = ("bf16 q/k/v/O with fp16 P·V; the seq_lens line cuts batch 1 at "
+                       f"{REF_SEQ_LENS[1]} tokens (the active-block FLOP count is not reduced)")
+        extra_cfg["reference_conditions"] = ref
+
+        # The long-context mixed workload (B1 H16 T16384, rows of 1-26 blocks varying by head):
+        # a parity configuration, timed for information (outside the geomean), with the work
+        # plan the shim makes for it and without one (the kernel's built-in order).
+        mq, mk, mv, mrp, mrpd, mcid = mixed
+        G = mw.B * mw.H * mw.nqb
+        m_out = torch.empty_like(mq)
+        m_lse = torch.empty((mw.B, mw.H, mw.T), device=dev, dtype=torch.float32)
+
+        def mixed_builtin():
+            _native.fwd(mq.data_ptr(), mk.data_ptr(), mv.data_ptr(), mrpd.data_ptr(),
+                        mcid.data_ptr(), None, m_out.data_ptr(), m_lse.data_ptr(), mw.B, mw.H,
+                        mw.T, D, mcid.shape[-1], _native.FP16, None, 0, stream.cuda_stream)
+
+        mfns = [lambda: block_sparse_attn_fwd(mq, mk, mv, mrpd, mcid, None), mixed_builtin]
+        warm(mfns, args.min_warmup_s)
+        t_plan, t_builtin = time_calls(mfns, args.steps, stream)
+        mp, mb = float(np.median(t_plan)), float(np.median(t_builtin))
+        mfl = P.active_blocks(mrp) * FLOP_PER_BLOCK
+        sched = _native.plan_host(mrp, mw.B, mw.H, mw.nqb)
+        extra_cfg["other_workloads"] = {"mixed": {
+            "B": mw.B, "H": mw.H, "T": mw.T, "active_blocks": P.active_blocks(mrp),
+            "median_ms": round(mp, 4), "tflops": round(mfl / mp / 1e9, 1),
+            "frac_peak": round(mfl / mp / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "work_plan_slots": None if sched is None else int(len(sched)), "items": G,
+            "builtin_order_median_ms": round(mb, 4),
+            "ratio_plan_to_builtin": round(mp / mb, 4)}}
+        del mixed, mq, mk, mv
 
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
@@ -455,6 +560,9 @@ def main() -> int:
                               "packets and dispatch gap included)"),
         "algorithmic_flop_per_launch": int(sum(flops) / len(flops)),
         "geomean_frac_peak": round(geomean([f["frac_peak"] for f in fam_out.values()]), 4),
+        "executed_mfma_flop_per_launch": int(sum(exec_flops) / len(exec_flops)),
+        "executed_mfma_frac": round((sum(exec_flops) / len(exec_flops)) / mean_launch / 1e9
+                                    / PEAK_FP16_TFLOPS, 4),
     }
 
     out = {
@@ -476,17 +584,20 @@ def main() -> int:
                         "3 families: sliding w8 / global 4 + local 4 / retrieval diag+prev+14",
             "B": B, "H": H, "T": T, "D": D, "block": 128,
             "families": fam_out,
-            "latency_timing": "HIP events around each call on the launch stream; median over "
-                              "the timed steps per family",
-            "analytic_rows": analytic,
-            "other_workloads": others,
+            "latency_timing": (f"HIP events around each call on the launch stream; the timed "
+                               f"steps split into {groups} consecutive groups, per family the "
+                               f"median over the groups of the median within each group"),
+            **extra_cfg,
             "input_seed": args.seed,
             "pattern_seed": P.PATTERN_SEED,
         },
         "roofline": roofline,
+        "profile": {"family_dispatches": (args.warmup + extra + args.steps) * len(P.FAMILIES),
+                    "order": list(P.FAMILIES)},
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(fams, inputs, args.cpu_heads, args.cpu_c_heads)
+        out["cpu_baseline"] = cpu_baseline(fams, inputs, args.cpu_heads, args.cpu_c_heads,
+                                           args.cpu_runs)
     print(json.dumps(out), flush=True)
     return 0
 

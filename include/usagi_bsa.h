@@ -21,6 +21,9 @@
  *   - seq_lens: int32 [B] or NULL (NULL: every sequence has length T). Query rows at or past
  *     seq_len get O = 0 and LSE = -inf (kernels/v7_blockptr_warpspec.py:63-67, 138-148).
  *   - lse: float32 [B, H, T], natural-log log-sum-exp of the scaled scores, or NULL to skip.
+ *   - sched / n_slots: an optional work plan from usagi_bsa_plan (device copy of its int32 array
+ *     and its return value), or NULL / 0 for the kernel's built-in order. Any plan of the same
+ *     CSR gives bit-identical results: it only decides which GPU slot runs which query block.
  *   - stream: a hipStream_t (NULL = the default stream). The launch is asynchronous.
  *   - Return: 0 on success; a negative USAGI_BSA_E* code for a rejected argument; a positive
  *     hipError_t value when the HIP runtime reports an error. usagi_bsa_last_error() gives a
@@ -37,6 +40,8 @@ extern "C" {
 
 #define USAGI_BSA_BLOCK 128
 #define USAGI_BSA_HEAD_DIM 128
+/* Capacity of the sched array usagi_bsa_plan needs for B*H*(T/128) items. */
+#define USAGI_BSA_PLAN_CAP(n_items) (2 * (int64_t)(n_items) + 8)
 
 enum usagi_bsa_dtype {
   USAGI_BSA_FP16 = 0, /* fp16 q/k/v/out (the build's contract) */
@@ -58,7 +63,21 @@ int usagi_bsa_fwd(const void* q, const void* k, const void* v,
                   const int32_t* row_ptr, const int32_t* col_idx, const int32_t* seq_lens,
                   void* out, float* lse,
                   int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
-                  int32_t max_nnz, int32_t dtype, void* stream);
+                  int32_t max_nnz, int32_t dtype, const int32_t* sched, int32_t n_slots,
+                  void* stream);
+
+/* Forward pass with the generic CSR walk of kernels/v1_baseline.py:331-406 (launched by its
+ * _run_csr, v1:411-441): every entry of a row is attended, in any order, with no implicit
+ * diagonal; an entry equal to the query block takes the causal mask, keys at or past seq_len
+ * are masked, and an empty row (or a row of fully masked entries) gives O = 0 and LSE = -inf.
+ * Entries are clamped to [0, T/128) for memory safety. Same arguments and conventions as
+ * usagi_bsa_fwd (a plan for it comes from usagi_bsa_plan with generic = 1). */
+int usagi_bsa_fwd_generic(const void* q, const void* k, const void* v,
+                          const int32_t* row_ptr, const int32_t* col_idx,
+                          const int32_t* seq_lens, void* out, float* lse,
+                          int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
+                          int32_t max_nnz, int32_t dtype, const int32_t* sched,
+                          int32_t n_slots, void* stream);
 
 /* Forward pass over an analytic pattern instead of a CSR: query block qb attends the global
  * prefix 0 .. n_global-1 and the window max(0, qb-window+1) .. qb (deduplicated; the diagonal is
@@ -73,15 +92,27 @@ int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
                          int32_t dtype, void* stream);
 
 /* Host-side CSR validator over HOST copies of row_ptr / col_idx; no counterpart in the reference,
- * which does not validate its input (kernels/v7_blockptr_warpspec.py:155-191). It checks the preconditions
- * under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-111 equals
- * block-mask ∧ causal attention: row_ptr[0] == 0, monotone, row_ptr[nqb] <= max_nnz, every row
- * non-empty, strictly ascending, every entry in [0, qb], and the last entry == qb.
- * Returns 0, or USAGI_BSA_ECSR with the first offending (b, h, qb) in usagi_bsa_last_error(). */
+ * which does not validate its input (kernels/v7_blockptr_warpspec.py:155-191). It checks the
+ * preconditions under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-136
+ * equals block-mask ∧ causal attention: row_ptr[0] == 0, every row non-empty and within
+ * max_nnz, its last entry == qb, and the entries before it distinct and in [0, qb) (in any
+ * order: the walk's result does not depend on it). Returns 0, or USAGI_BSA_ECSR with the first
+ * offending (b, h, qb) in usagi_bsa_last_error(). */
 int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
                         int32_t batch, int32_t heads, int32_t num_q_blocks, int32_t max_nnz);
 
-/* Version string of this library, e.g. "usagi_bsa 0.1.0 gfx950". No counterpart in the
+/* Work plan over a HOST copy of row_ptr; no counterpart in the reference, whose grid is
+ * (nqb, B*H) in index order (kernels/v7_blockptr_warpspec.py:178-179). When rows of different
+ * heads differ in length, it spreads the work evenly over the GPU's 8 XCDs (each XCD on a few
+ * heads at a time, its longest rows first) and writes the slot -> item table (item
+ * b*H*nqb + h*nqb + qb, or -1 for an idle slot) to sched[0 .. n_slots). generic: 1 plans for
+ * usagi_bsa_fwd_generic, 0 for usagi_bsa_fwd. sched_cap >= USAGI_BSA_PLAN_CAP(B*H*nqb).
+ * Returns n_slots (> 0), 0 when the built-in order is already balanced (launch with sched
+ * NULL), or a negative USAGI_BSA_E* code. */
+int usagi_bsa_plan(const int32_t* row_ptr, int32_t batch, int32_t heads, int32_t num_q_blocks,
+                   int32_t generic, int32_t* sched, int32_t sched_cap);
+
+/* Version string of this library, e.g. "usagi_bsa 0.2.0 gfx950". No counterpart in the
  * reference (its module has no version). */
 const char* usagi_bsa_version(void);
 

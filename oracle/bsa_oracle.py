@@ -3,7 +3,7 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module, and only
 to check results (or as the timed CPU baseline); the product path (usagi_amd) never imports it.
 
-Two restatements of the reference's math:
+Three restatements of the reference's math:
 
   dense_masked()  fp32 (or fp64) softmax attention over the dense token mask
                   block_mask(CSR) ∧ causal ∧ key < seq_len, rows t >= seq_len -> O = 0,
@@ -16,11 +16,16 @@ Two restatements of the reference's math:
                   with the causal / seq_len / q-valid mask (v7:111-136), scores scaled after
                   the dot in fp32 (v7:92), P rounded to fp16 before P·V (v7:107), m initialised
                   to -1e30 (v7:73), O = acc / l_safe and LSE = m·ln2 + ln l (v7:138-148).
+  blockwise_v1()  the generic walk of kernels/v1_baseline.py:360-406 (every entry, any order,
+                  an entry equal to qb causally masked, keys past seq_len masked, no implicit
+                  diagonal).
 
 Pins (tests/test_oracle.py): fp64 brute force over explicitly enumerated key sets, the golden
 fixtures in tests/golden/ (written by that brute force), torch's scaled_dot_product_attention
 for a full lower-triangular CSR and for a diagonal-only CSR, and invariants (V constant,
-Q = 0, query row 0, LSE = logsumexp, order invariance of the off-diagonal entries).
+Q = 0, query row 0, LSE = logsumexp, order invariance of the off-diagonal entries); for
+blockwise_v1 also the fixture golden_generic_t384.npz of an fp64 brute force over key
+multisets, and duplicating every entry leaving O unchanged while adding ln 2 to LSE.
 """
 
 from __future__ import annotations
@@ -163,6 +168,72 @@ def blockwise_v7(q, k, v, row_ptr, col_idx, seq_lens=None, round_p_fp16: bool = 
             out[b, h, q_pos] = o
             ls = np.where(l_i > 0, m_i * np.float32(LN2) + np.log(l_safe), -np.inf)
             lse[b, h, q_pos] = np.where(q_valid, ls, -np.inf)              # v7:146-147
+    return out, lse
+
+
+V1_MUTATIONS = ("diag_unmasked", "no_key_mask", "dedupe")
+
+
+def blockwise_v1(q, k, v, row_ptr, col_idx, seq_lens=None, round_p_fp16: bool = True,
+                 heads: list[tuple[int, int]] | None = None, _mutation: str | None = None):
+    """The reference's generic CSR walk (kernels/v1_baseline.py:360-406) restated in numpy
+    (fp32): every entry of the row in its order (v1:370-376), no implicit diagonal; an entry
+    equal to qb is causally masked (v1:382-383); keys at or past seq_len and invalid query rows
+    are masked for every entry (v1:385-386); a row with no visible key gives O = 0 and
+    LSE = -inf (v1:398-406, output pre-filled with zeros / -inf at v1:421-422). Entries outside
+    [0, nqb) are clamped into it, as the build does (the reference would read outside K/V).
+    `_mutation` plants one of V1_MUTATIONS for the test suite's pins."""
+    qn, kn, vn = _np(q), _np(k), _np(v)
+    B, H, T, D = qn.shape
+    nqb = T // BLOCK
+    rp = np.asarray(row_ptr).reshape(B, H, nqb + 1)
+    ci = np.asarray(col_idx).reshape(B, H, -1)
+    sl = np.full(B, T) if seq_lens is None else np.asarray(seq_lens).reshape(B)
+    out = np.full((B, H, T, D), np.nan, dtype=np.float32)
+    lse = np.full((B, H, T), np.nan, dtype=np.float32)
+    offs = np.arange(BLOCK)
+    qk_scale = np.float32(QK_SCALE)
+    pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
+    v16 = _fp16_round(vn) if round_p_fp16 else vn
+    for b, h in pairs:
+        seq_len = int(sl[b])
+        for qb in range(nqb):
+            q_start = qb * BLOCK
+            q_pos = q_start + offs
+            if q_start >= seq_len:                                         # v1:360
+                out[b, h, q_pos] = 0.0
+                lse[b, h, q_pos] = -np.inf
+                continue
+            q_valid = q_pos < seq_len                                      # v1:362
+            qt = qn[b, h, q_pos]
+            m_i = np.full(BLOCK, -1e30, dtype=np.float32)                  # v1:366
+            l_i = np.zeros(BLOCK, dtype=np.float32)
+            acc = np.zeros((BLOCK, D), dtype=np.float32)
+            rs, re = int(rp[b, h, qb]), int(rp[b, h, qb + 1])              # v1:370-373
+            kbs = [min(max(int(x), 0), nqb - 1) for x in ci[b, h, rs:re]]
+            if _mutation == "dedupe":
+                kbs = sorted(set(kbs))
+            for kb in kbs:                                                 # v1:375-376
+                k_pos = kb * BLOCK + offs
+                s = (qt @ kn[b, h, k_pos].T) * qk_scale                    # v1:380
+                mask = np.broadcast_to(q_valid[:, None], s.shape).copy()   # v1:386
+                if kb == qb and _mutation != "diag_unmasked":              # v1:382-383
+                    mask &= offs[None, :] <= offs[:, None]
+                if _mutation != "no_key_mask":                             # v1:385
+                    mask &= k_pos[None, :] < seq_len
+                s = np.where(mask, s, -np.inf).astype(np.float32)
+                m_new = np.maximum(m_i, s.max(axis=1))                    # v1:388-389
+                alpha = np.exp2(m_i - m_new)                               # v1:390
+                p = np.exp2(s - m_new[:, None])                            # v1:391
+                l_i = alpha * l_i + p.sum(axis=1)                          # v1:392
+                pv = _fp16_round(p) if round_p_fp16 else p                 # v1:395
+                acc = acc * alpha[:, None] + pv @ v16[b, h, k_pos]
+                m_i = m_new
+            l_safe = np.where(l_i > 0, l_i, 1.0).astype(np.float32)        # v1:398
+            o = np.where(q_valid[:, None], acc / l_safe[:, None], 0.0)     # v1:399-404
+            out[b, h, q_pos] = o
+            ls = np.where(l_i > 0, m_i * np.float32(LN2) + np.log(l_safe), -np.inf)
+            lse[b, h, q_pos] = np.where(q_valid, ls, -np.inf)              # v1:405-406
     return out, lse
 
 

@@ -14,6 +14,11 @@
  *   scores = dot * QK_SCALE in fp32 after the dot (v7:92); exp2 online softmax (v7:96-100);
  *   P (and V) rounded to fp16 before P·V when round_p_fp16 != 0 (v7:107);
  *   O = acc / l_safe, invalid rows 0, LSE = m·ln2 + ln(l_safe) or -inf (v7:138-148).
+ * With walk = 1 it follows the generic walk of kernels/v1_baseline.py:360-406 instead: every
+ * entry of the row in its order (v1:375-376), with no implicit diagonal; an entry equal to qb takes
+ * the causal mask c <= r (v1:382-383), every entry masks keys at or past seq_len and invalid
+ * query rows (v1:385-386). Entries outside [0, nqb) are clamped into it (the reference would
+ * read outside K/V there; the build clamps the same way).
  * The argument list mirrors usagi_bsa_fwd (include/usagi_bsa.h) with host float arrays.
  */
 #include <math.h>
@@ -39,7 +44,7 @@ static float round_fp16(float x) {
 int oracle_bsa_fwd(const float* q, const float* k, const float* v, const int32_t* row_ptr,
                    const int32_t* col_idx, const int32_t* seq_lens, float* out, float* lse,
                    int32_t batch, int32_t heads, int32_t seq_len_max, int32_t head_dim,
-                   int32_t max_nnz, int32_t round_p_fp16) {
+                   int32_t max_nnz, int32_t round_p_fp16, int32_t walk) {
   if (!q || !k || !v || !row_ptr || !out || batch <= 0 || heads <= 0 || seq_len_max <= 0 ||
       seq_len_max % BLK || head_dim <= 0 || max_nnz < 0 || (max_nnz > 0 && !col_idx))
     return -1;
@@ -75,9 +80,17 @@ int oracle_bsa_fwd(const float* q, const float* k, const float* v, const int32_t
     const int rs = rp[qb], re = rp[qb + 1];
     const int n_off = re - rs - 1 > 0 ? re - rs - 1 : 0;
     const int32_t* cols = col_idx ? col_idx + bh * max_nnz + rs : NULL;
-    for (int j = 0; j <= n_off; ++j) {
-      const int diag = (j == n_off);
-      const int kb = diag ? qb : cols[j];
+    /* v7: off-diagonal entries then the implicit diagonal (n_off + 1 blocks); v1: every entry. */
+    const int n_blk = walk ? (cols && re - rs > 0 ? re - rs : 0) : n_off + 1;
+    for (int j = 0; j < n_blk; ++j) {
+      int kb, diag;
+      if (walk) {
+        kb = cols[j] < 0 ? 0 : (cols[j] >= nqb ? nqb - 1 : cols[j]);
+        diag = kb == qb;
+      } else {
+        diag = (j == n_off);
+        kb = diag ? qb : cols[j];
+      }
       const int k_start = kb * BLK;
       const float* kp = k + base + (size_t)k_start * D;
       const float* vp = v + base + (size_t)k_start * D;
@@ -91,6 +104,7 @@ int oracle_bsa_fwd(const float* q, const float* k, const float* v, const int32_t
           float sc = dot * qk_scale;
           int keep = q_valid;
           if (diag) keep = keep && (c <= r) && (k_start + c < seq_len);
+          if (walk) keep = keep && (k_start + c < seq_len);
           s[r * BLK + c] = keep ? sc : -INFINITY;
         }
       }

@@ -21,15 +21,17 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib = ctypes.CDLL(path)
     p = ctypes.c_void_p
     i32 = ctypes.c_int32
-    lib.oracle_bsa_fwd.argtypes = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32]
+    lib.oracle_bsa_fwd.argtypes = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, i32]
     lib.oracle_bsa_fwd.restype = ctypes.c_int
     if path == LIB:
         _lib = lib
     return lib
 
 
-def fwd(q, k, v, row_ptr, col_idx, seq_lens=None, round_p_fp16: bool = True, lib=None):
-    """q/k/v: float arrays [B,H,T,D] (any float dtype; converted to fp32). Returns (O, LSE)."""
+def fwd(q, k, v, row_ptr, col_idx, seq_lens=None, round_p_fp16: bool = True, lib=None,
+        generic: bool = False):
+    """q/k/v: float arrays [B,H,T,D] (any float dtype; converted to fp32). Returns (O, LSE).
+    generic: the order-free walk of kernels/v1_baseline.py:360-406 instead of v7's."""
     lib = lib or load()
     qn = np.ascontiguousarray(q, dtype=np.float32)
     kn = np.ascontiguousarray(k, dtype=np.float32)
@@ -45,7 +47,7 @@ def fwd(q, k, v, row_ptr, col_idx, seq_lens=None, round_p_fp16: bool = True, lib
                             ci.ctypes.data if max_nnz else None,
                             sl.ctypes.data if sl is not None else None,
                             out.ctypes.data, lse.ctypes.data, B, H, T, D, max_nnz,
-                            1 if round_p_fp16 else 0)
+                            1 if round_p_fp16 else 0, 1 if generic else 0)
     if rc != 0:
         raise ValueError(f"oracle_bsa_fwd rejected its arguments (rc={rc})")
     return out, lse

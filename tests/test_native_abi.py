@@ -40,24 +40,29 @@ def test_version_and_empty_error():
     assert _native.version().startswith("usagi_bsa ") and "gfx950" in _native.version()
 
 
-def _fwd(**over):
+def _fwd(generic=False, **over):
     args = dict(q=1, k=1, v=1, rp=1, ci=1, sl=None, o=1, lse=None, B=1, H=1, T=128, D=128,
-                nnz=1, dtype=0, stream=None)
+                nnz=1, dtype=0, sched=None, slots=0, stream=None)
     args.update(over)
     lib = _native.load()
+    f = lib.usagi_bsa_fwd_generic if generic else lib.usagi_bsa_fwd
     p = lambda x: None if x is None else ctypes.c_void_p(x)  # noqa: E731
-    return lib.usagi_bsa_fwd(p(args["q"]), p(args["k"]), p(args["v"]), p(args["rp"]), p(args["ci"]),
-                             p(args["sl"]), p(args["o"]), p(args["lse"]), args["B"], args["H"],
-                             args["T"], args["D"], args["nnz"], args["dtype"], p(args["stream"]))
+    return f(p(args["q"]), p(args["k"]), p(args["v"]), p(args["rp"]), p(args["ci"]),
+             p(args["sl"]), p(args["o"]), p(args["lse"]), args["B"], args["H"], args["T"],
+             args["D"], args["nnz"], args["dtype"], p(args["sched"]), args["slots"],
+             p(args["stream"]))
 
 
+@pytest.mark.parametrize("generic", [False, True])
 @pytest.mark.parametrize("over,code", [
     (dict(q=None), -1), (dict(o=None), -1), (dict(rp=None), -1),
     (dict(dtype=7), -2), (dict(D=64), -3), (dict(T=100), -4), (dict(T=0), -4),
     (dict(B=0), -1), (dict(H=-1), -1), (dict(nnz=-1), -1), (dict(ci=None, nnz=3), -1),
+    # a plan must cover at least every item (here 1) and at most USAGI_BSA_PLAN_CAP(1) = 10 slots
+    (dict(sched=1, slots=0), -1), (dict(sched=1, slots=11), -1),
 ])
-def test_argument_errors_are_reported_before_any_launch(over, code):
-    assert _fwd(**over) == code
+def test_argument_errors_are_reported_before_any_launch(over, code, generic):
+    assert _fwd(generic=generic, **over) == code
     assert _native.last_error()
 
 

@@ -11,6 +11,11 @@ challenge harness), so the oracle is pinned by checks that do not restate its fo
   * the reference's own walk restated twice (numpy blockwise_v7, C bsa_ref.c) agreeing with the
     dense-masked oracle;
   * planted mistakes (oracle._mutation) that each of these checks must reject.
+The generic walk (blockwise_v1 and the C walk with generic=True) is pinned by its own fixture
+(golden_generic_t384.npz: fp64 over key multisets), by agreeing with the dense-masked oracle on
+rows in any order with or without their diagonal, and by duplicating every entry (O unchanged,
+LSE + ln 2). The PyTorch CPU oracle (oracle/torch_dense.py, the timed CPU baseline) is pinned by
+the fixtures and by agreeing with bsa_oracle.dense_masked.
 """
 
 from __future__ import annotations
@@ -23,7 +28,7 @@ import pytest
 import torch
 
 from oracle import bsa_oracle as O
-from oracle import c_ref
+from oracle import c_ref, torch_dense
 from tests._helpers import assert_close
 from usagi_amd import patterns as P
 
@@ -236,7 +241,7 @@ def test_c_restatement_under_address_sanitizer(tmp_path):
     code = f"""
 import numpy as np, sys
 sys.path.insert(0, {repr(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))})
-from oracle import c_ref
+from oracle import c_ref, torch_dense
 from usagi_amd import patterns as P
 rp, ci = P.random_csr(2, 2, 384, 0.6, 1)
 rng = np.random.default_rng(0)
@@ -249,3 +254,133 @@ print("ok")
     res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env,
                          timeout=600)
     assert res.returncode == 0 and "ok" in res.stdout, res.stderr[-2000:]
+
+
+# ------------------------------------------------------------------------------ PyTorch CPU oracle
+
+
+@pytest.mark.parametrize("name", ["golden_families_t512.npz", "golden_seqlens_t256.npz"])
+def test_torch_dense_matches_golden(name):
+    g = np.load(os.path.join(GOLDEN, name))
+    q, k, v = (torch.from_numpy(g[x]) for x in ("q", "k", "v"))
+    o, lse = torch_dense.dense_masked(q, k, v, torch.from_numpy(g["row_ptr"]),
+                                      torch.from_numpy(g["col_idx"]), g["seq_lens"])
+    assert_close(o.numpy(), g["out"], atol=2e-5, rtol=2e-5)
+    assert_close(lse.numpy(), g["lse"], atol=2e-5, rtol=2e-5, what="LSE")
+
+
+def test_torch_dense_matches_numpy_dense_on_a_head_subset():
+    B, H, T = 2, 3, 1280  # two query slabs of 1024 rows, the second one partial
+    rp, ci = P.retrieval_csr(B, H, T, 4, 8)
+    q, k, v = P.make_qkv(B, H, T, seed=60)
+    heads = [(0, 2), (1, 0)]
+    sl = np.array([T, 1000])
+    o, lse = torch_dense.dense_masked(q, k, v, torch.from_numpy(rp), torch.from_numpy(ci), sl,
+                                      heads=heads)
+    od, ld = O.dense_masked(q, k, v, rp, ci, sl, heads=heads)
+    for b, h in heads:
+        assert_close(o[b, h].numpy(), od[b, h], atol=1e-5, rtol=1e-5)
+        assert_close(lse[b, h].numpy(), ld[b, h], atol=1e-5, rtol=1e-5, what="LSE")
+    assert torch.isnan(o[0, 0]).all()  # heads outside the subset stay NaN
+
+
+# ------------------------------------------------------------------------------ generic walk (v1)
+
+
+def _golden_generic():
+    g = np.load(os.path.join(GOLDEN, "golden_generic_t384.npz"))
+    return g, (g["q"], g["k"], g["v"], g["row_ptr"], g["col_idx"], g["seq_lens"])
+
+
+@pytest.mark.parametrize("impl", ["blockwise", "blockwise_fp32", "c"])
+def test_generic_walk_matches_golden(impl):
+    g, args = _golden_generic()
+    if impl == "blockwise":
+        o, lse = O.blockwise_v1(*args)
+        tol = 2e-3  # P rounded to fp16 before P·V, as in the reference (v1:395)
+    elif impl == "blockwise_fp32":
+        o, lse = O.blockwise_v1(*args, round_p_fp16=False)
+        tol = 2e-5
+    else:
+        o, lse = c_ref.fwd(*[a.astype(np.float32) if a.dtype == np.float16 else a for a in args],
+                           generic=True)
+        tol = 2e-3
+    assert_close(o, g["out"], atol=tol, rtol=tol)
+    assert_close(lse, g["lse"], atol=tol, rtol=tol, what="LSE")
+
+
+def test_generic_golden_covers_its_cases():
+    g, _ = _golden_generic()
+    # head 1, qb 0 is an empty row: O = 0, LSE = -inf for every row of it
+    assert np.all(g["out"][:, 1, :128] == 0) and np.all(np.isneginf(g["lse"][:, 1, :128]))
+    # batch 1 has seq_len 200: query block 2 is cut entirely
+    assert np.all(g["out"][1, :, 256:] == 0) and np.all(np.isneginf(g["lse"][1, :, 256:]))
+    assert np.all(np.isfinite(g["lse"][0, 0]))
+
+
+@pytest.mark.parametrize("mutation", O.V1_MUTATIONS)
+def test_generic_pins_reject_planted_mistakes(mutation):
+    g, args = _golden_generic()
+    o, lse = O.blockwise_v1(*args, round_p_fp16=False, _mutation=mutation)
+    assert not (np.allclose(o, g["out"], atol=2e-3, rtol=2e-3)
+                and np.allclose(lse, g["lse"], atol=2e-3, rtol=2e-3)), mutation
+
+
+def _shuffled_rows(rp, ci, seed, drop_diag_every=0):
+    """Every row permuted (diagonal anywhere); with drop_diag_every = n, every n-th row loses
+    its diagonal. Returns a new (row_ptr, col_idx)."""
+    rng = np.random.default_rng(seed)
+    B, H, n1 = rp.shape
+    rows = []
+    for b in range(B):
+        rows.append([])
+        for h in range(H):
+            rr = []
+            for i in range(n1 - 1):
+                r = [int(x) for x in ci[b, h, rp[b, h, i]:rp[b, h, i + 1]]]
+                if drop_diag_every and i % drop_diag_every == 1:
+                    r = [x for x in r if x != i]
+                rr.append([int(x) for x in rng.permutation(r)])
+            rows[b].append(rr)
+    return P.rows_to_csr(rows)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_generic_walk_equals_dense_on_rows_in_any_order(seed):
+    """Rows of distinct blocks at or below the query block, in any order, with or without
+    their diagonal: the generic walk is the dense block mask ∧ causal ∧ seq_len attention."""
+    B, H, T = 2, 2, 640
+    rp, ci = P.random_csr(B, H, T, 0.6, 30 + seed)
+    rp2, ci2 = _shuffled_rows(rp, ci, seed, drop_diag_every=3)
+    q, k, v = _rand_qkv(B, H, T, 40 + seed)
+    sl = np.array([T, 333])
+    od, ld = O.dense_masked(q, k, v, rp2, ci2, sl)
+    ob, lb = O.blockwise_v1(q, k, v, rp2, ci2, sl)
+    oc, lc = c_ref.fwd(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), rp2, ci2,
+                       sl, generic=True)
+    assert_close(ob, od)
+    assert_close(lb, ld, what="LSE")
+    assert_close(oc, ob, atol=1e-4, rtol=1e-4)
+    assert_close(lc, lb, atol=1e-5, rtol=1e-5, what="LSE")
+    # the v7 walk agrees where its precondition holds (every row ends with its diagonal)
+    o7, l7 = O.blockwise_v7(q, k, v, rp, ci, sl)
+    o1, l1 = O.blockwise_v1(q, k, v, rp, ci, sl)
+    assert_close(o1, o7, atol=5e-4, rtol=5e-4)
+    assert_close(l1, l7, atol=1e-5, rtol=1e-5, what="LSE")
+
+
+def test_generic_walk_duplicated_entries_add_ln2():
+    """Listing every entry twice doubles every weight: O is unchanged, LSE grows by ln 2."""
+    B, H, T = 1, 2, 512
+    rp, ci = P.random_csr(B, H, T, 0.5, 5)
+    rows = [[[r + r for r in P.csr_rows(rp, ci, b, h)] for h in range(H)] for b in range(B)]
+    rp2, ci2 = P.rows_to_csr(rows)
+    q, k, v = _rand_qkv(B, H, T, 9)
+    o1, l1 = O.blockwise_v1(q, k, v, rp, ci, round_p_fp16=False)
+    o2, l2 = O.blockwise_v1(q, k, v, rp2, ci2, round_p_fp16=False)
+    assert_close(o2, o1, atol=1e-5, rtol=1e-5)
+    assert_close(l2 - math.log(2.0), l1, atol=1e-5, rtol=1e-5, what="LSE")
+    oc, lc = c_ref.fwd(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), rp2, ci2,
+                       round_p_fp16=False, generic=True)
+    assert_close(oc, o2, atol=1e-5, rtol=1e-5)
+    assert_close(lc, l2, atol=1e-5, rtol=1e-5, what="LSE")

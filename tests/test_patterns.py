@@ -69,8 +69,12 @@ def test_mixed_heads():
 def _broken(kind):
     rp, ci = P.sliding_csr(1, 2, 512, 3)
     rp, ci = rp.copy(), ci.copy()
-    if kind == "unsorted":
-        ci[0, 1, rp[0, 1, 3]:rp[0, 1, 3] + 2] = ci[0, 1, rp[0, 1, 3]:rp[0, 1, 3] + 2][::-1]
+    if kind == "duplicate":
+        ci[0, 1, rp[0, 1, 3] + 1] = ci[0, 1, rp[0, 1, 3]]
+    elif kind == "diagonal_in_the_middle":
+        ci[0, 1, rp[0, 1, 3] + 1:rp[0, 1, 4]] = ci[0, 1, rp[0, 1, 3] + 1:rp[0, 1, 4]][::-1]
+    elif kind == "negative_block":
+        ci[0, 1, rp[0, 1, 3]] = -1
     elif kind == "no_diagonal_last":
         ci[0, 0, rp[0, 0, 2] - 1] = 0
     elif kind == "future_block":
@@ -85,7 +89,8 @@ def _broken(kind):
     return rp, ci
 
 
-@pytest.mark.parametrize("kind", ["unsorted", "no_diagonal_last", "future_block", "empty_row",
+@pytest.mark.parametrize("kind", ["duplicate", "diagonal_in_the_middle", "negative_block",
+                                  "no_diagonal_last", "future_block", "empty_row",
                                   "row_ptr_start", "row_ptr_overflow"])
 def test_validators_reject_malformed_csr(kind):
     rp, ci = _broken(kind)
@@ -93,6 +98,19 @@ def test_validators_reject_malformed_csr(kind):
         P.validate_csr(rp, ci, 512)
     with pytest.raises(ValueError, match="malformed CSR"):
         _native.check_csr_host(rp, ci, 1, 2, 4, ci.shape[-1])
+
+
+def test_validators_accept_rows_in_any_order_before_the_diagonal():
+    """The walk does not depend on the order of the entries before the diagonal."""
+    rp, ci = P.global_csr(1, 2, 1024, 2, 3)
+    ci = ci.copy()
+    rng = np.random.default_rng(0)
+    for h in range(2):
+        for i in range(8):
+            a, b = rp[0, h, i], rp[0, h, i + 1] - 1
+            ci[0, h, a:b] = rng.permutation(ci[0, h, a:b])
+    P.validate_csr(rp, ci, 1024)
+    _native.check_csr_host(rp, ci, 1, 2, 8, ci.shape[-1])
 
 
 @pytest.mark.parametrize("seed", range(6))

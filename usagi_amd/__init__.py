@@ -2,7 +2,8 @@
 
 The reference's submission-module names are re-exported here:
 VARIANT_MANIFEST, setup, block_sparse_attn_fwd (kernels/v7_blockptr_warpspec.py:24, 201, 251),
-plus block_sparse_attn_fwd_window, the analytic window / window + global-prefix path
+plus block_sparse_attn_fwd_generic, the order-free CSR walk (kernels/v1_baseline.py:331-406),
+and block_sparse_attn_fwd_window, the analytic window / window + global-prefix path
 (kernels/v1_baseline.py:141-322).
 """
 
@@ -11,8 +12,10 @@ from .submission import (  # noqa: F401
     HEAD_DIM,
     VARIANT_MANIFEST,
     block_sparse_attn_fwd,
+    block_sparse_attn_fwd_generic,
     block_sparse_attn_fwd_window,
+    clear_csr_cache,
     setup,
 )
 
-__version__ = "0.1.0"
+__version__ = "0.2.0"

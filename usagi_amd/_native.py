@@ -18,8 +18,10 @@ BF16 = 1
 
 EXPORTED_SYMBOLS = (
     "usagi_bsa_fwd",
+    "usagi_bsa_fwd_generic",
     "usagi_bsa_fwd_window",
     "usagi_bsa_check_csr",
+    "usagi_bsa_plan",
     "usagi_bsa_version",
     "usagi_bsa_last_error",
 )
@@ -46,12 +48,17 @@ def load() -> ctypes.CDLL:
     lib = ctypes.CDLL(LIB_PATH)
     p = ctypes.c_void_p
     i32 = ctypes.c_int32
-    lib.usagi_bsa_fwd.argtypes = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, p]
+    fwd_args = [p, p, p, p, p, p, p, p, i32, i32, i32, i32, i32, i32, p, i32, p]
+    lib.usagi_bsa_fwd.argtypes = fwd_args
     lib.usagi_bsa_fwd.restype = ctypes.c_int
+    lib.usagi_bsa_fwd_generic.argtypes = fwd_args
+    lib.usagi_bsa_fwd_generic.restype = ctypes.c_int
     lib.usagi_bsa_fwd_window.argtypes = [p, p, p, i32, i32, p, p, p, i32, i32, i32, i32, i32, p]
     lib.usagi_bsa_fwd_window.restype = ctypes.c_int
     lib.usagi_bsa_check_csr.argtypes = [p, p, i32, i32, i32, i32]
     lib.usagi_bsa_check_csr.restype = ctypes.c_int
+    lib.usagi_bsa_plan.argtypes = [p, i32, i32, i32, i32, p, i32]
+    lib.usagi_bsa_plan.restype = ctypes.c_int
     lib.usagi_bsa_version.argtypes = []
     lib.usagi_bsa_version.restype = ctypes.c_char_p
     lib.usagi_bsa_last_error.argtypes = []
@@ -74,10 +81,12 @@ def check(code: int) -> None:
 
 
 def fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr, out_ptr, lse_ptr,
-        batch, heads, seq_len, head_dim, max_nnz, dtype, stream) -> None:
-    check(load().usagi_bsa_fwd(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr,
-                               out_ptr, lse_ptr, batch, heads, seq_len, head_dim, max_nnz,
-                               dtype, stream))
+        batch, heads, seq_len, head_dim, max_nnz, dtype, sched_ptr, n_slots, stream,
+        generic: bool = False) -> None:
+    lib = load()
+    f = lib.usagi_bsa_fwd_generic if generic else lib.usagi_bsa_fwd
+    check(f(q_ptr, k_ptr, v_ptr, row_ptr_ptr, col_idx_ptr, seq_lens_ptr, out_ptr, lse_ptr, batch,
+            heads, seq_len, head_dim, max_nnz, dtype, sched_ptr, n_slots, stream))
 
 
 def fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr, out_ptr, lse_ptr,
@@ -85,6 +94,26 @@ def fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr, out_ptr, lse
     check(load().usagi_bsa_fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr,
                                       out_ptr, lse_ptr, batch, heads, seq_len, head_dim, dtype,
                                       stream))
+
+
+def plan_cap(n_items: int) -> int:
+    """USAGI_BSA_PLAN_CAP of include/usagi_bsa.h."""
+    return 2 * n_items + 8
+
+
+def plan_host(row_ptr, batch: int, heads: int, nqb: int, generic: bool = False):
+    """Work plan over a host (numpy) row_ptr: an int32 slot -> item array, or None when the
+    kernel's built-in order is already balanced."""
+    import numpy as np
+
+    rp = np.ascontiguousarray(row_ptr, dtype=np.int32)
+    cap = plan_cap(batch * heads * nqb)
+    sched = np.empty(cap, dtype=np.int32)
+    n = load().usagi_bsa_plan(rp.ctypes.data, batch, heads, nqb, 1 if generic else 0,
+                              sched.ctypes.data, cap)
+    if n < 0:
+        raise NativeError(n, last_error())
+    return sched[:n].copy() if n else None
 
 
 def check_csr_host(row_ptr, col_idx, batch: int, heads: int, nqb: int, max_nnz: int) -> None:

@@ -14,7 +14,9 @@ import sys
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 INCLUDE_DIR = os.path.join(REPO_DIR, "include")
-SRC = os.path.join(PKG_DIR, "csrc", "bsa_fwd.hip")
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+# The kernels and their launch ABI (HIP), and the host-only validator and work planner.
+SRCS = [os.path.join(CSRC_DIR, "bsa_fwd.hip"), os.path.join(CSRC_DIR, "bsa_plan.cpp")]
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libusagi_bsa.so")
 ARCH = "gfx950"
@@ -27,7 +29,8 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc, PATH)")
 
 
-def hipcc_command(src: str = SRC, out: str = LIB_PATH, extra: list[str] | None = None) -> list[str]:
+def hipcc_command(srcs: list[str] | None = None, out: str = LIB_PATH,
+                  extra: list[str] | None = None) -> list[str]:
     return [
         hipcc_path(),
         f"--offload-arch={ARCH}",
@@ -38,8 +41,9 @@ def hipcc_command(src: str = SRC, out: str = LIB_PATH, extra: list[str] | None =
         # Packed FP32 VALU forms are kept out of the device code.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", INCLUDE_DIR,
+        "-I", CSRC_DIR,
         *(extra or []),
-        src,
+        *(srcs or SRCS),
         "-o", out,
     ]
 

@@ -6,8 +6,8 @@ prefix, sliding window + retrieval; scored by the geometric mean of family media
 layout follows the reference wrapper: row_ptr [B, H, nqb+1] with offsets local to each (b, h)
 row, col_idx [B, H, max_nnz] padded (kernels/v7_blockptr_warpspec.py:77-80, 172-174).
 Every generated row is ascending, has all key blocks <= the query block and ends with the
-diagonal, which is the precondition of the implicit-diagonal walk
-(kernels/v7_blockptr_warpspec.py:83, 111).
+diagonal, which meets the precondition of the implicit-diagonal walk
+(kernels/v7_blockptr_warpspec.py:83, 111; see validate_csr).
 """
 
 from __future__ import annotations
@@ -126,9 +126,10 @@ def active_blocks(row_ptr: np.ndarray) -> int:
 
 
 def validate_csr(row_ptr: np.ndarray, col_idx: np.ndarray, T: int) -> None:
-    """Raise ValueError unless every row is non-empty, strictly ascending, within [0, qb] and
-    ends with the diagonal (the implicit-diagonal precondition of
-    kernels/v7_blockptr_warpspec.py:83-111)."""
+    """Raise ValueError unless every row is non-empty, ends with its diagonal, and lists the
+    blocks before it at most once each, all in [0, qb) (any order): the precondition under
+    which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-136 equals
+    block-mask ∧ causal attention. Same rules as usagi_bsa_check_csr."""
     B, H, n1 = row_ptr.shape
     nqb = T // BLOCK
     if n1 != nqb + 1:
@@ -139,16 +140,19 @@ def validate_csr(row_ptr: np.ndarray, col_idx: np.ndarray, T: int) -> None:
             rp = row_ptr[b, h]
             if rp[0] != 0:
                 raise ValueError(f"(b={b},h={h}): row_ptr[0] = {rp[0]}")
-            if rp[-1] > max_nnz:
-                raise ValueError(f"(b={b},h={h}): row_ptr[-1] = {rp[-1]} > max_nnz {max_nnz}")
             for i in range(nqb):
+                if rp[i + 1] <= rp[i]:
+                    raise ValueError(f"(b={b},h={h},qb={i}): empty or decreasing row")
+                if rp[i + 1] > max_nnz:
+                    raise ValueError(f"(b={b},h={h},qb={i}): row_ptr {rp[i + 1]} > max_nnz {max_nnz}")
                 r = col_idx[b, h, rp[i]:rp[i + 1]]
-                if len(r) == 0:
-                    raise ValueError(f"(b={b},h={h},qb={i}): empty row")
-                if np.any(np.diff(r) <= 0):
-                    raise ValueError(f"(b={b},h={h},qb={i}): not strictly ascending")
-                if r[0] < 0 or r[-1] != i:
-                    raise ValueError(f"(b={b},h={h},qb={i}): entries outside [0,{i}] or diagonal not last")
+                if r[-1] != i:
+                    raise ValueError(f"(b={b},h={h},qb={i}): last entry {r[-1]} is not the diagonal")
+                off = r[:-1]
+                if len(off) and (off.min() < 0 or off.max() >= i):
+                    raise ValueError(f"(b={b},h={h},qb={i}): entries before the diagonal outside [0,{i})")
+                if len(np.unique(off)) != len(off):
+                    raise ValueError(f"(b={b},h={h},qb={i}): a key block listed twice")
 
 
 # ---------------------------------------------------------------------------------------------

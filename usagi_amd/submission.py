@@ -5,23 +5,35 @@
     setup(suite_specs, device, variants)
     block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens) -> (O, LSE)
 
+plus block_sparse_attn_fwd_generic (the order-free CSR walk of kernels/v1_baseline.py:331-406)
+and block_sparse_attn_fwd_window (analytic window rows, kernels/v1_baseline.py:141-322).
+
 Differences from the reference, all deliberate:
   * fp16 q/k/v/O is the primary dtype; bf16 is also accepted (O in bf16, P·V in fp16 as in
     kernels/v7_blockptr_warpspec.py:107).
   * The launch goes through the C ABI of libusagi_bsa.so (compiled ahead of time for gfx950)
-    instead of a Triton JIT launch; there is no metadata cache keyed on data_ptr()
-    (kernels/v7_blockptr_warpspec.py:167-176): int32 contiguous CSR tensors are used in place,
-    anything else is converted on every call.
+    instead of a Triton JIT launch.
+  * The first call with a given pair of CSR tensors copies them to the host once (one
+    synchronisation), checks every row (block_sparse_attn_fwd raises ValueError on a row that
+    is empty, unsorted, outside [0, qb] or not ending with its diagonal: the reference's walk,
+    kernels/v7_blockptr_warpspec.py:83-111, would silently attend future tokens there) and
+    plans the work order over the GPU. Later calls with the same tensor objects, unmodified,
+    reuse that (the reference memoises converted metadata on data_ptr() alone,
+    kernels/v7_blockptr_warpspec.py:167-176; here the key also holds the shapes, dtypes,
+    torch's in-place version counters and the tensor objects themselves). A CSR changed
+    outside torch (e.g. through a NumPy view of its memory) needs clear_csr_cache().
+    USAGI_BSA_VALIDATE=0 (read at import) skips the check.
   * `setup` loads the ahead-of-time library first, so a missing build fails at setup time; like
     the reference it returns None without doing anything for a non-GPU device
-    (kernels/v7_blockptr_warpspec.py:202-203), and block_sparse_attn_fwd then rejects CPU
-    tensors (there is no CPU path).
+    (kernels/v7_blockptr_warpspec.py:202-203), and the entry points then reject CPU tensors
+    (there is no CPU path).
 """
 
 from __future__ import annotations
 
-import math
 import os
+import weakref
+from collections import OrderedDict
 
 import torch
 
@@ -29,17 +41,59 @@ from . import _native
 
 BLOCK_SIZE = 128
 HEAD_DIM = 128
-_SCORE_SCALE = 1.0 / math.sqrt(HEAD_DIM)
-_LOG2E = math.log2(math.e)
-_QK_SCALE = _SCORE_SCALE * _LOG2E
-_LN2 = math.log(2.0)
 
 VARIANT_MANIFEST = [{"name": "default"}]
 
-# USAGI_BSA_VALIDATE=1 copies the CSR to the host on every call and checks it (synchronises).
-VALIDATE_CSR = os.environ.get("USAGI_BSA_VALIDATE", "0") not in ("", "0")
+VALIDATE_CSR = os.environ.get("USAGI_BSA_VALIDATE", "1") not in ("", "0")
 
 _DTYPE_CODES = {torch.float16: _native.FP16, torch.bfloat16: _native.BF16}
+
+_CSR_CACHE_SIZE = 64
+
+
+class _CsrEntry:
+    """What the first call learnt about one (row_ptr, col_idx) pair: the tensors it was made
+    for (weak references) and the device copy of its work plan (None: built-in order)."""
+
+    __slots__ = ("row_ptr", "col_idx", "sched", "n_slots")
+
+    def __init__(self, row_ptr, col_idx, sched, n_slots):
+        self.row_ptr = weakref.ref(row_ptr)
+        self.col_idx = weakref.ref(col_idx)
+        self.sched = sched
+        self.n_slots = n_slots
+
+
+_csr_cache: "OrderedDict[tuple, _CsrEntry]" = OrderedDict()
+
+
+def clear_csr_cache() -> None:
+    """Forget every checked and planned CSR (the next call with any CSR checks it again)."""
+    _csr_cache.clear()
+
+
+def _tensor_key(t: torch.Tensor) -> tuple:
+    return (t.device, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, t._version)
+
+
+def _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic: bool) -> _CsrEntry:
+    key = (generic, dev, _tensor_key(row_ptr), _tensor_key(col_idx))
+    e = _csr_cache.get(key)
+    if e is not None and e.row_ptr() is row_ptr and e.col_idx() is col_idx:
+        _csr_cache.move_to_end(key)
+        return e
+    rp = row_ptr.detach().reshape(B, H, nqb + 1).to("cpu", torch.int32).contiguous().numpy()
+    max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
+    ci = col_idx.detach().reshape(B, H, max_nnz).to("cpu", torch.int32).contiguous().numpy()
+    if not generic and VALIDATE_CSR:
+        _native.check_csr_host(rp, ci, B, H, nqb, max_nnz)
+    sched = _native.plan_host(rp, B, H, nqb, generic)
+    dsched = torch.from_numpy(sched).to(dev) if sched is not None else None
+    e = _CsrEntry(row_ptr, col_idx, dsched, 0 if sched is None else len(sched))
+    _csr_cache[key] = e
+    while len(_csr_cache) > _CSR_CACHE_SIZE:
+        _csr_cache.popitem(last=False)
+    return e
 
 
 def _as_int32_device(t: torch.Tensor, device: torch.device, shape: tuple) -> torch.Tensor:
@@ -73,31 +127,27 @@ def _check_inputs(q, k, v):
     return B, H, T, D
 
 
-def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
-    """Block-sparse causal attention forward.
-
-    q, k, v: [B, H, T, 128] fp16 (or bf16) on the GPU.
-    row_ptr: [B, H, T/128 + 1] integer, offsets local to each (b, h) row of col_idx.
-    col_idx: [B, H, max_nnz] integer; each row ascending with the diagonal last.
-    seq_lens: [B] integer (or None = all T).
-    Returns (O [B, H, T, 128] in q.dtype, LSE [B, H, T] float32), as
-    kernels/v7_blockptr_warpspec.py:191.
-    """
+def _run_csr(q, k, v, row_ptr, col_idx, seq_lens, generic: bool):
     B, H, T, D = _check_inputs(q, k, v)
     dev = q.device
     nqb = T // BLOCK_SIZE
+    if not isinstance(row_ptr, torch.Tensor) or not isinstance(col_idx, torch.Tensor):
+        raise TypeError("row_ptr and col_idx must be torch.Tensors")
+    if row_ptr.numel() != B * H * (nqb + 1):
+        raise ValueError(f"row_ptr must hold [B, H, T/128 + 1] = [{B}, {H}, {nqb + 1}] values, "
+                         f"got shape {tuple(row_ptr.shape)}")
+    max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
+    if col_idx.numel() != B * H * max_nnz:
+        raise ValueError(f"col_idx must be [B, H, max_nnz], got shape {tuple(col_idx.shape)}")
+    plan = _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic)
     q = q.contiguous()
     k = k.contiguous()
     v = v.contiguous()
     rp = _as_int32_device(row_ptr, dev, (B, H, nqb + 1))
-    max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
     ci = _as_int32_device(col_idx, dev, (B, H, max_nnz))
     sl = None
     if seq_lens is not None:
         sl = _as_int32_device(torch.as_tensor(seq_lens), dev, (B,))
-
-    if VALIDATE_CSR:
-        _native.check_csr_host(rp.cpu().numpy(), ci.cpu().numpy(), B, H, nqb, max_nnz)
 
     out = torch.empty((B, H, T, D), device=dev, dtype=q.dtype)
     lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
@@ -105,9 +155,31 @@ def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
         stream = torch.cuda.current_stream(dev).cuda_stream
         _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), rp.data_ptr(),
                     ci.data_ptr() if max_nnz else None, sl.data_ptr() if sl is not None else None,
-                    out.data_ptr(), lse.data_ptr(), B, H, T, D, max_nnz,
-                    _DTYPE_CODES[q.dtype], stream)
+                    out.data_ptr(), lse.data_ptr(), B, H, T, D, max_nnz, _DTYPE_CODES[q.dtype],
+                    plan.sched.data_ptr() if plan.sched is not None else None, plan.n_slots,
+                    stream, generic=generic)
     return out, lse
+
+
+def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
+    """Block-sparse causal attention forward (kernels/v7_blockptr_warpspec.py:251-252).
+
+    q, k, v: [B, H, T, 128] fp16 (or bf16) on the GPU.
+    row_ptr: [B, H, T/128 + 1] integer, offsets local to each (b, h) row of col_idx.
+    col_idx: [B, H, max_nnz] integer; each row strictly ascending with the diagonal last.
+    seq_lens: [B] integer (or None = all T).
+    Returns (O [B, H, T, 128] in q.dtype, LSE [B, H, T] float32), as
+    kernels/v7_blockptr_warpspec.py:191.
+    """
+    return _run_csr(q, k, v, row_ptr, col_idx, seq_lens, generic=False)
+
+
+def block_sparse_attn_fwd_generic(q, k, v, row_ptr, col_idx, seq_lens):
+    """The generic CSR walk of kernels/v1_baseline.py:331-406: every entry of a row in any
+    order, no implicit diagonal (an entry equal to the query block is causally masked, an empty
+    row gives O = 0 and LSE = -inf), keys at or past seq_len masked. Same tensors and returns
+    as block_sparse_attn_fwd; rows are not checked (any content is defined)."""
+    return _run_csr(q, k, v, row_ptr, col_idx, seq_lens, generic=True)
 
 
 def block_sparse_attn_fwd_window(q, k, v, window, n_global=0, seq_lens=None):
