@@ -18,8 +18,10 @@ docs/OPTIMIZATION_JOURNAL.md:135, 189-190).
 The warmup is W steps plus, if needed, more whole steps until S seconds have passed (reported as
 warmup_extra_steps): from idle the GPU takes tens of ms of sustained load to reach steady clocks.
 
-Prints one JSON line. Besides the contract fields, after the timed steps: per family launch_ms
-(mean per-call event time, the roofline's launch duration) and burst_ms (back-to-back bursts);
+Prints one JSON line. Besides the contract fields: per family launch_ms (the roofline's launch
+duration: the mean kernel duration over a second block of the same steps, right after the timed
+ones, from events attached to each kernel dispatch itself; a call's latency adds a few us of
+launch gap and event packets to it) and, after that, burst_ms (back-to-back bursts);
 config.full_seq_variant (seq_lens None, the kernel with the length masks compiled out, against
 seq_lens of all T); config.analytic_rows (the analytic window path against the CSR path);
 config.reference_conditions (bf16 inputs, and bf16 with variable seq_lens, as the reference was
@@ -163,11 +165,12 @@ KERNEL = "bsa_fwd_dma_kernel"
 CALIB_KERNEL = "neg"
 
 
-def pmc_summary(paths, calib_mib: int, bench_json: str | None) -> int:
+def pmc_summary(paths, calib_mib: int, bench_json) -> int:
     """Per-family averages of rocprofv3 --pmc counters for the attention kernel.
 
     The first profile.family_dispatches dispatches of the kernel (read from the JSON line the
-    profiled bench run printed, --bench-json) are its warmup and timed steps, issued in family
+    profiled bench run printed, --bench-json: one file per counter CSV, in the same order, or
+    one file for all of them) are its warmup and timed steps, issued in family
     order (sliding, global, retrieval) every step, so dispatch i of them belongs to
     FAMILIES[i % 3]; later dispatches (bursts, the other lines of the bench) are left out. The
     calibration kernel is the elementwise negation of --calib-copy-mib MiB (it reads and writes
@@ -185,19 +188,24 @@ def pmc_summary(paths, calib_mib: int, bench_json: str | None) -> int:
     if not calib_mib:
         print("--pmc-summary needs the --calib-copy-mib value of the profiled run", file=sys.stderr)
         return 2
-    if not bench_json:
-        print("--pmc-summary needs --bench-json (the JSON line of the profiled run)", file=sys.stderr)
+    if not bench_json or len(bench_json) not in (1, len(paths)):
+        print("--pmc-summary needs --bench-json: the JSON line of each profiled run (one file per "
+              "counter CSV, or one for all)", file=sys.stderr)
         return 2
-    with open(bench_json) as f:
-        line = [x for x in f.read().splitlines() if x.startswith("{")][-1]
-    n_fam = int(json.loads(line)["profile"]["family_dispatches"])
+    n_fams = []
+    for jp in bench_json:
+        with open(jp) as f:
+            line = [x for x in f.read().splitlines() if x.startswith("{")][-1]
+        n_fams.append(int(json.loads(line)["profile"]["family_dispatches"]))
+    if len(n_fams) == 1:
+        n_fams = n_fams * len(paths)
     known_kib = calib_mib * 1024.0
     sums: dict = {}
     durs: dict = {}
     calib: dict = {}
     calib_name = None
     n_xcc, n_simd = 8, 1024
-    for path in paths:
+    for path, n_fam in zip(paths, n_fams):
         with open(path) as f:
             rows = list(csv.DictReader(f))
         by_disp: dict = {}
@@ -239,8 +247,8 @@ def pmc_summary(paths, calib_mib: int, bench_json: str | None) -> int:
                 t = durs.setdefault(fam, [0.0, 0])
                 t[0] += dur_of[d]
                 t[1] += 1
-    print(f"kernel {KERNEL}: the first {n_fam} dispatches of each pass (warmup and timed steps); "
-          f"calibration kernel: {calib_name}")
+    print(f"kernel {KERNEL}: the first {'/'.join(str(n) for n in n_fams)} dispatches of the "
+          f"passes (their warmup and timed steps); calibration kernel: {calib_name}")
     for cname, val in sorted(calib.items()):
         print(f"calibration {cname} {val:.1f}")
     factor = {}
@@ -351,7 +359,8 @@ def main() -> int:
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="summarise rocprofv3 --pmc counter_collection.csv files of a run of "
                          "this script (made with --calib-copy-mib) and exit; no GPU is used")
-    ap.add_argument("--bench-json", help="with --pmc-summary: the JSON output of that run")
+    ap.add_argument("--bench-json", nargs="+",
+                    help="with --pmc-summary: the JSON output of each profiled run")
     args = ap.parse_args()
 
     if args.pmc_summary:
@@ -418,6 +427,15 @@ def main() -> int:
 
     stream = torch.cuda.current_stream(dev)
     ev = {n: [event_pair() for _ in range(args.steps)] for n in P.FAMILIES}
+    # Events attached to each kernel dispatch (usagi_bsa_time_next_launch) time the kernel
+    # itself, without the launch gap and event packets that events around a call include. They
+    # add a few us to the call around them, so they are used in a second block of the same
+    # steps right after the timed ones, never in the timed steps.
+    kev = {n: [event_pair() for _ in range(args.steps)] for n in P.FAMILIES}
+    for pairs in kev.values():
+        for a, b in pairs:  # torch creates its events at their first record
+            a.record(stream)
+            b.record(stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
@@ -428,6 +446,12 @@ def main() -> int:
             b.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    for s in range(args.steps):
+        for name in P.FAMILIES:
+            ka, kb = kev[name][s]
+            _native.time_next_launch(ka.cuda_event, kb.cuda_event)
+            call(name)
+    torch.cuda.synchronize()
 
     groups = max(1, min(args.repeats, args.steps))
     bounds = np.linspace(0, args.steps, groups + 1).astype(int)
@@ -436,6 +460,7 @@ def main() -> int:
     launch_ms = {}
     for name in P.FAMILIES:
         ts = np.array([a.elapsed_time(b) for a, b in ev[name]])
+        kts = np.array([a.elapsed_time(b) for a, b in kev[name]])
         group_meds = [float(np.median(ts[bounds[g]:bounds[g + 1]])) for g in range(groups)]
         med = float(np.median(group_meds))
         fl = P.active_blocks(fams[name][0]) * FLOP_PER_BLOCK
@@ -443,13 +468,14 @@ def main() -> int:
         medians.append(med)
         flops.append(fl)
         exec_flops.append(efl)
-        launch_ms[name] = float(np.mean(ts))
+        launch_ms[name] = float(np.mean(kts))
         fam_out[name] = {
             "median_ms": round(med, 4),
             "group_medians_ms": [round(x, 4) for x in group_meds],
             "median_all_steps_ms": round(float(np.median(ts)), 4),
             "mean_ms": round(float(np.mean(ts)), 4),
             "launch_ms": round(launch_ms[name], 4),
+            "kernel_median_ms": round(float(np.median(kts)), 4),
             "active_blocks": P.active_blocks(fams[name][0]),
             "tflops": round(fl / med / 1e9, 1),
             "frac_peak": round(fl / med / 1e9 / PEAK_FP16_TFLOPS, 4),
@@ -555,9 +581,10 @@ def main() -> int:
                     if traffic and all(n in traffic for n in P.FAMILIES) else None),
         "kernel": "bsa_fwd_dma_kernel",
         "avg_launch_ms": round(mean_launch, 4),
-        "avg_launch_timing": ("HIP events around each call of the timed steps on the launch "
-                              "stream: mean per family, then mean over the families (event "
-                              "packets and dispatch gap included)"),
+        "avg_launch_timing": ("HIP events attached to each kernel dispatch (hipExtLaunchKernel via "
+                              "usagi_bsa_time_next_launch) over a block of the same steps run "
+                              "right after the timed ones: the kernel's own duration, mean per "
+                              "family, then mean over the families"),
         "algorithmic_flop_per_launch": int(sum(flops) / len(flops)),
         "geomean_frac_peak": round(geomean([f["frac_peak"] for f in fam_out.values()]), 4),
         "executed_mfma_flop_per_launch": int(sum(exec_flops) / len(exec_flops)),
@@ -593,6 +620,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "profile": {"family_dispatches": (args.warmup + extra + args.steps) * len(P.FAMILIES),
+                    "kernel_timing_dispatches": args.steps * len(P.FAMILIES),
                     "order": list(P.FAMILIES)},
     }
     if not args.no_cpu:

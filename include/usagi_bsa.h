@@ -112,6 +112,14 @@ int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
 int usagi_bsa_plan(const int32_t* row_ptr, int32_t batch, int32_t heads, int32_t num_q_blocks,
                    int32_t generic, int32_t* sched, int32_t sched_cap);
 
+/* Timing hook for benchmarks; no counterpart in the reference. The calling thread's next
+ * forward launch (any usagi_bsa_fwd* entry point) records start_event when its kernel starts
+ * and stop_event when it completes (hipExtLaunchKernel's events, attached to the dispatch
+ * itself), so their elapsed time is the kernel's own duration, without the launch gap and event
+ * packets that events recorded around the call include. hipEvent_t handles created with timing,
+ * either may be NULL; the setting is consumed by that one launch. Returns 0. */
+int usagi_bsa_time_next_launch(void* start_event, void* stop_event);
+
 /* Version string of this library, e.g. "usagi_bsa 0.2.0 gfx950". No counterpart in the
  * reference (its module has no version). */
 const char* usagi_bsa_version(void);

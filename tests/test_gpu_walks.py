@@ -211,3 +211,33 @@ def test_default_walk_rejects_a_row_whose_diagonal_is_not_last():
     oo, ol = c_generic(q, k, v, rp, ci)
     assert_close(o, oo)
     assert_close(lse, ol, what="LSE")
+
+
+# ------------------------------------------------------------------------------ timing hook
+
+
+def test_timing_hook_times_the_kernel_itself():
+    """usagi_bsa_time_next_launch attaches events to the next dispatch: their elapsed time is
+    positive and within the events recorded around the call, the result is unchanged, and the
+    setting is used by that one launch only."""
+    w = P.workloads()["sliding"]
+    rp, ci = w.csr()
+    q, k, v = (x.to(DEV) for x in P.make_qkv(w.B, w.H, w.T, seed=17))
+    drp, dci = _dev(rp), _dev(ci)
+    st = torch.cuda.current_stream()
+    o1, l1 = block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in ev:
+        e.record(st)
+    torch.cuda.synchronize()
+    print("case timing hook", flush=True)
+    ev[0].record(st)
+    _native.time_next_launch(ev[1].cuda_event, ev[2].cuda_event)
+    o2, l2 = block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    ev[3].record(st)
+    o3, l3 = block_sparse_attn_fwd(q, k, v, drp, dci, None)  # no events attached any more
+    torch.cuda.synchronize()
+    kernel_ms = ev[1].elapsed_time(ev[2])
+    call_ms = ev[0].elapsed_time(ev[3])
+    assert 0.0 < kernel_ms <= call_ms, (kernel_ms, call_ms)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2) and torch.equal(o1, o3)

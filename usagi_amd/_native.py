@@ -22,6 +22,7 @@ EXPORTED_SYMBOLS = (
     "usagi_bsa_fwd_window",
     "usagi_bsa_check_csr",
     "usagi_bsa_plan",
+    "usagi_bsa_time_next_launch",
     "usagi_bsa_version",
     "usagi_bsa_last_error",
 )
@@ -59,6 +60,8 @@ def load() -> ctypes.CDLL:
     lib.usagi_bsa_check_csr.restype = ctypes.c_int
     lib.usagi_bsa_plan.argtypes = [p, i32, i32, i32, i32, p, i32]
     lib.usagi_bsa_plan.restype = ctypes.c_int
+    lib.usagi_bsa_time_next_launch.argtypes = [p, p]
+    lib.usagi_bsa_time_next_launch.restype = ctypes.c_int
     lib.usagi_bsa_version.argtypes = []
     lib.usagi_bsa_version.restype = ctypes.c_char_p
     lib.usagi_bsa_last_error.argtypes = []
@@ -94,6 +97,13 @@ def fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr, out_ptr, lse
     check(load().usagi_bsa_fwd_window(q_ptr, k_ptr, v_ptr, window, n_global, seq_lens_ptr,
                                       out_ptr, lse_ptr, batch, heads, seq_len, head_dim, dtype,
                                       stream))
+
+
+def time_next_launch(start_event, stop_event) -> None:
+    """Attach two hipEvent_t handles (ints, e.g. torch.cuda.Event(enable_timing=True).cuda_event
+    of events recorded once already) to this thread's next forward launch: they then time the
+    kernel itself."""
+    check(load().usagi_bsa_time_next_launch(start_event or None, stop_event or None))
 
 
 def plan_cap(n_items: int) -> int:

@@ -35,6 +35,7 @@
 //     running max as it stands and checks the row sum of P (a sum <= 2^12 proves every P finite
 //     in fp16); the other two move the running max only when it grows by more than 2^8.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -689,14 +690,15 @@ void bsa_fwd_dma_kernel(Args a) {
         *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
       }
     }
-    // Only this wave's rows: LDS operations of one wave complete in order, no barrier.
+    // Only this wave's rows: LDS operations of one wave complete in order, no barrier. O is
+    // streamed out non-temporally: nothing in this launch reads it again, and K/V keep the L2.
     uint16_t* oblk = a.o + base + (size_t)(q0 + 32 * wave) * kHd;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = 4 * i + (lane >> 4);
       const int c = lane & 15;
       const u32x4 x = *(const u32x4*)(stage + row * 256 + 16 * (c ^ (row & 15)));
-      *(u32x4*)(oblk + (size_t)row * kHd + 8 * c) = x;
+      __builtin_nontemporal_store(x, (u32x4*)(oblk + (size_t)row * kHd + 8 * c));
     }
   }
   if (a.lse && lh == 0) {
@@ -767,6 +769,10 @@ int prepare_csr(Args& a, const int32_t* row_ptr, const int32_t* col_idx, int32_t
   return USAGI_BSA_OK;
 }
 
+// Events to attach to the calling thread's next launch (usagi_bsa_time_next_launch).
+thread_local hipEvent_t g_next_start = nullptr;
+thread_local hipEvent_t g_next_stop = nullptr;
+
 template <bool kBf16, int kRows>
 int launch(const Args& a, int slots, hipStream_t s) {
   const void* fn = a.seq_lens
@@ -774,9 +780,16 @@ int launch(const Args& a, int slots, hipStream_t s) {
                        : reinterpret_cast<const void*>(&bsa_fwd_dma_kernel<kBf16, kRows, true>);
   Args arg = a;
   void* params[] = {&arg};
-  // hipLaunchKernel reports this launch's own status (a prior error left on the thread by
+  // Both launch calls report this launch's own status (a prior error left on the thread by
   // another HIP call is neither taken for it nor cleared).
-  const hipError_t err = hipLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s);
+  hipError_t err;
+  if (g_next_start || g_next_stop) {
+    hipEvent_t e0 = g_next_start, e1 = g_next_stop;
+    g_next_start = g_next_stop = nullptr;
+    err = hipExtLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s, e0, e1, 0);
+  } else {
+    err = hipLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s);
+  }
   if (err != hipSuccess) return usagi_bsa_fail((int)err, "kernel launch failed: %s", hipGetErrorString(err));
   return USAGI_BSA_OK;
 }
@@ -789,6 +802,13 @@ int launch_dtype(const Args& a, int32_t dtype, int slots, void* stream) {
 }
 
 }  // namespace
+
+extern "C" int usagi_bsa_time_next_launch(void* start_event, void* stop_event) {
+  usagi_bsa_clear_error();
+  g_next_start = static_cast<hipEvent_t>(start_event);
+  g_next_stop = static_cast<hipEvent_t>(stop_event);
+  return USAGI_BSA_OK;
+}
 
 extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
                              const int32_t* row_ptr, const int32_t* col_idx,
