@@ -8,32 +8,33 @@
 // over fp32 scores scaled AFTER the dot product (v7:92, v7:96-100); P is rounded to fp16 before
 // P·V (v7:107). O = acc / l and LSE = m·ln2 + ln l (v7:138-148).
 //
-// Three kernels share that structure:
-//   bsa_fwd_dma_kernel<bf16, window>  the default for fp16 and bf16: K/V tiles DMA'd HBM -> LDS,
-//                           V read transposed out of LDS, two workgroups per CU, diagonal block
-//                           first, speculative softmax (see the comment at the kernel). With
-//                           window = true the rows are a window (+ global prefix) computed in
-//                           the kernel instead of read from the CSR (usagi_bsa_fwd_window).
-//   bsa_fwd_kernel<bf16>    register-staged K/V (global -> VGPR -> LDS, V transposed and
-//                           converted to fp16 on the way in); USAGI_BSA_FP16_KERNEL=staged.
-//   bsa_fwd_split_kernel    fp16, one workgroup per CU, each wave 64 rows x 64 keys, K/V
-//                           double-buffered; USAGI_BSA_FP16_KERNEL=split.
+// One kernel template, bsa_fwd_dma_kernel<kBf16, kRows, kFullSeq>:
+//   kBf16     fp16 or bf16 inputs (bf16: Q·K^T in bf16, V converted to fp16 in LDS, P·V in fp16
+//             as v7:107 does, O written in bf16).
+//   kRows     where a query block's key blocks come from: kRowsCsr (the v7 walk above),
+//             kRowsWindow (a window + global prefix computed in the kernel, no CSR reads) or
+//             kRowsGeneric (the v1 walk, kernels/v1_baseline.py:360-406: every entry in any
+//             order, no implicit diagonal, an entry equal to qb causally masked).
+//   kFullSeq  no seq_lens (every sequence has length T): the length masks are compiled out.
 //
-// Common MI355X design points (not a translation of the Triton program):
-//   * One 256-thread workgroup (4 wave64s) per (b*h, qb); each wave owns 32 query rows (the
-//     split kernel: 64 rows and half the keys).
+// MI355X design points (not a translation of the Triton program):
+//   * One 256-thread workgroup (4 wave64s) per (b*h, qb), or per slot of a host work plan; each
+//     wave owns 32 query rows; two workgroups per CU (64 KiB LDS, <= 240 VGPRs each).
 //   * Everything is computed transposed so that one lane owns one query row:
 //       S^T[key][q] = K · Q^T      (MFMA A = K rows from LDS, B = Q fragment in VGPRs)
-//       O^T[d][q]  += V^T · P^T    (MFMA A = V^T rows from LDS, B = P taken straight from the
-//                                   S^T accumulator registers, no LDS round trip)
+//       O^T[d][q]  += V^T · P^T    (MFMA A = V^T read with ds_read_b64_tr_b16 from the row-major
+//                                   V tile, B = P taken straight from the S^T accumulators)
 //     With v_mfma_f32_32x32x16_{f16,bf16}, lane l holds query (l % 32); the other 64 keys of
 //     that query sit in lane l ^ 32, so the row max is one v_permlane32_swap and the running
 //     row sum needs no cross-lane work until the epilogue.
-//   * Work order (item_coords): longest row first; when B*H is a multiple of 8, head-major per
-//     XCD, so the K/V tiles of the head an XCD is walking stay in its L2.
-//   * The O rescale is skipped for almost every block: the DMA kernel computes P with the
-//     running max as it stands and checks the row sum of P (a sum <= 2^12 proves every P finite
-//     in fp16); the other two move the running max only when it grows by more than 2^8.
+//   * K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), XOR-swizzled,
+//     and their DMA pieces are interleaved with the other product's MFMAs.
+//   * Work order without a plan (item_coords): query blocks from the last one down; when B*H is
+//     a multiple of 8, head-major per XCD, so the K/V tiles of the head an XCD is walking stay in
+//     its L2.
+//   * The diagonal block goes first and sets the exact row max; later blocks compute P with the
+//     running max as it stands and accept it when the row sum of P is <= 2^12 (which proves every
+//     P finite in fp16), so the O rescale is skipped for almost every block.
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -55,8 +56,6 @@ namespace {
 constexpr int kBlk = USAGI_BSA_BLOCK;    // rows per query / key block
 constexpr int kHd = USAGI_BSA_HEAD_DIM;  // head dimension
 constexpr int kThreads = 256;            // 4 wave64s
-constexpr int kRow = kHd + 8;            // halfs per padded LDS row (272 B)
-constexpr float kTau = 8.0f;             // lazy-rescale threshold, log2 units
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kSpecSum = 4096.0f;      // acceptance bound of a speculative P row sum
 
@@ -91,11 +90,11 @@ struct Args {
 };
 
 // Work item (workgroup index) -> (query block, b*h) when no plan is given.
-// head_major == 0: longest rows first over the whole grid (query blocks in descending order,
-//   b*h fastest).
+// head_major == 0: query blocks in descending order (for causal window patterns the longest
+//   rows first), b*h fastest.
 // head_major == 1 (B*H a multiple of 8): workgroups are dealt to the 8 XCDs round-robin by
 //   index, so item i runs on XCD i % 8; each XCD walks its heads x, x+8, ... one at a time, and
-//   within a head takes the query blocks longest row first. The key/value tiles of the head being
+//   within a head takes the query blocks in descending order. The key/value tiles of the head being
 //   walked (4 MiB at T = 8192) then stay in that XCD's L2 while all its query blocks read them.
 __device__ __forceinline__ void item_coords(const Args& a, int item, int& qb, int& bh) {
   if (a.head_major) {
@@ -479,7 +478,7 @@ void bsa_fwd_dma_kernel(Args a) {
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
 
-    // ---- masks (v7:94, v7:119-122), row max, lazy rescale
+    // ---- masks (v7:94, v7:119-122), row max, speculative P
     if constexpr (kDiag) {
       // Key tiles below the wave's own (t < wave) are visible to all its rows, its own tile
       // (t == wave) takes the causal mask, and the tiles above (t > wave) were skipped by the
