@@ -178,8 +178,9 @@ typedef __attribute__((address_space(1))) const void global_cvoid;
 // (s_waitcnt vmcnt + s_barrier) before any wave reads the tile.
 template <int kImm>
 __device__ __forceinline__ void dma_16b(const void* gbase, uint32_t voff, uint32_t lds_addr) {
-  // M0 holds the LDS destination; it is declared clobbered, so the compiler keeps nothing of
-  // its own in M0 across the statement.
+  // M0 holds the LDS destination. It is listed as clobbered, but the compiler does not preserve
+  // a reserved register across an asm statement; this is safe because nothing else in the
+  // kernel uses M0 (tests/test_device_code.py checks the assembly for that).
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
