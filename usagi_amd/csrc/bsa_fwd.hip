@@ -130,9 +130,18 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-__device__ __forceinline__ uint16_t to_out_bits(float x, bool bf16) {
-  if (bf16) return __builtin_bit_cast(uint16_t, (__bf16)x);
-  return __builtin_bit_cast(uint16_t, (_Float16)x);
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// Two fp32 -> one dword of two fp16 / bf16 (v_cvt_pk_*_f32, round to nearest even). O is
+// rounded twice, to fp32 by the multiply with 1/l and then to the output type, as the reference's
+// fp32 division and cast do.
+template <bool kBf16>
+__device__ __forceinline__ uint32_t pack_out(float x, float y) {
+  if constexpr (kBf16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{x, y}, bf16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{x, y}, half2));
+  }
 }
 
 template <bool kBf16>
@@ -675,17 +684,27 @@ void bsa_fwd_dma_kernel(Args a) {
   // K tile is free.
   {
     char* stage = (char*)k_lds + wave * 8192;  // 32 rows x 256 B, chunk c at c ^ (row % 16)
+    // Rows past seq_len were computed on whatever their Q holds: their O is cleared by a select
+    // (never a multiply), and inv is 0 for them.
+    if constexpr (!kFullSeq) {
+      if (!__all(qvalid)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o_acc[u][r] = qvalid ? o_acc[u][r] : 0.0f;
+        }
+      }
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 wv;
-        // Rows past seq_len were computed on whatever their Q holds: select, never multiply.
         float ov[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = qvalid ? o_acc[u][4 * g + e] * inv : 0.0f;
-        wv[0] = (uint32_t)to_out_bits(ov[0], kBf16) | ((uint32_t)to_out_bits(ov[1], kBf16) << 16);
-        wv[1] = (uint32_t)to_out_bits(ov[2], kBf16) | ((uint32_t)to_out_bits(ov[3], kBf16) << 16);
+        for (int e = 0; e < 4; ++e) ov[e] = o_acc[u][4 * g + e] * inv;
+        wv[0] = pack_out<kBf16>(ov[0], ov[1]);
+        wv[1] = pack_out<kBf16>(ov[2], ov[3]);
         // d = 32u + 8g + 4lh .. +3: 16-byte chunk 4u + g, half lh.
         *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
       }
