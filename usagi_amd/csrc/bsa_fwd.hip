@@ -121,17 +121,16 @@ __device__ __forceinline__ float wave_pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Two bf16 (one dword) -> two fp16 (one dword), round to nearest even.
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two bf16 (one dword) -> two fp16 (one dword), round to nearest even: each bf16 widens exactly
+// to fp32 (its bits in the upper half), then one v_cvt_pk_f16_f32 packs the pair.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   const float lo = __uint_as_float(w << 16);
   const float hi = __uint_as_float(w & 0xffff0000u);
-  const _Float16 a = (_Float16)lo;
-  const _Float16 b = (_Float16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, half2));
 }
-
-typedef float floatx2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 // Two fp32 -> one dword of two fp16 / bf16 (v_cvt_pk_*_f32, round to nearest even). O is
 // rounded twice, to fp32 by the multiply with 1/l and then to the output type, as the reference's
 // fp32 division and cast do.
