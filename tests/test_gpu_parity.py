@@ -253,6 +253,32 @@ def test_rows_longer_than_64_blocks():
         assert_close(lse[:, h:h + 1], ol, what=f"LSE[h={h}]")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_long_sequence(dtype):
+    """T = 32768 (256 query blocks): a global prefix, a window and random far blocks, rows of
+    up to 80 entries (past the 64-entry column chunk), seq_lens cutting inside a block; every
+    head against the fp32 walk."""
+    B, H, T = 1, 2, 128 * 256
+    rng = np.random.default_rng(31)
+
+    def row(b, h, i):
+        near = set(range(max(0, i - 7), i)) | set(range(min(4, i)))
+        far = rng.choice(i, size=min(i, 80 - 1 - len(near)), replace=False) if i > 100 else []
+        return sorted(near | {int(x) for x in far}) + [i]
+
+    rp, ci = P.make_csr(B, H, T, row)
+    assert int(np.diff(rp, axis=-1).max()) > 64
+    sl = [30000]
+    q, k, v = P.make_qkv(B, H, T, seed=32, dtype=dtype)
+    print(f"case long sequence T{T} {dtype} max row {int(np.diff(rp, axis=-1).max())}", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci, sl)
+    oo, ol = c_oracle(q, k, v, rp, ci, sl)
+    rtol = 2e-3 + (2.0 ** -9 if dtype == torch.bfloat16 else 0.0)  # bf16 O: half an ulp more
+    assert_close(o, oo, rtol=rtol)
+    assert_close(lse, ol, what="LSE")
+    assert np.all(o[:, :, 30000:] == 0) and np.all(np.isneginf(lse[:, :, 30000:]))
+
+
 def test_int64_csr_noncontiguous_inputs_and_list_seq_lens():
     B, H, T = 2, 3, 640
     rp, ci = P.retrieval_csr(B, H, T, 3, 4)
