@@ -15,9 +15,11 @@ Differences from the reference, all deliberate:
     instead of a Triton JIT launch.
   * The first call with a given pair of CSR tensors copies them to the host once (one
     synchronisation), checks every row (block_sparse_attn_fwd raises ValueError on a row that
-    is empty, unsorted, outside [0, qb] or not ending with its diagonal: the reference's walk,
-    kernels/v7_blockptr_warpspec.py:83-111, would silently attend future tokens there) and
-    plans the work order over the GPU. Later calls with the same tensor objects, unmodified,
+    is empty, repeats a block, lists a block outside [0, qb) before its last entry, or does not
+    end with its diagonal: the reference's walk, kernels/v7_blockptr_warpspec.py:83-111, would
+    silently attend future tokens or count a block twice there; the entries before the diagonal
+    may come in any order) and plans the work order over the GPU. Later calls with the same
+    tensor objects, unmodified,
     reuse that (the reference memoises converted metadata on data_ptr() alone,
     kernels/v7_blockptr_warpspec.py:167-176; here the key also holds the shapes, dtypes,
     torch's in-place version counters and the tensor objects themselves). A CSR changed
@@ -166,7 +168,8 @@ def block_sparse_attn_fwd(q, k, v, row_ptr, col_idx, seq_lens):
 
     q, k, v: [B, H, T, 128] fp16 (or bf16) on the GPU.
     row_ptr: [B, H, T/128 + 1] integer, offsets local to each (b, h) row of col_idx.
-    col_idx: [B, H, max_nnz] integer; each row strictly ascending with the diagonal last.
+    col_idx: [B, H, max_nnz] integer; each row lists distinct key blocks below its query block,
+        in any order, then the diagonal (the reference's rows are ascending, which qualifies).
     seq_lens: [B] integer (or None = all T).
     Returns (O [B, H, T, 128] in q.dtype, LSE [B, H, T] float32), as
     kernels/v7_blockptr_warpspec.py:191.
