@@ -19,10 +19,9 @@ Differences from the reference, all deliberate:
     end with its diagonal: the reference's walk, kernels/v7_blockptr_warpspec.py:83-111, would
     silently attend future tokens or count a block twice there; the entries before the diagonal
     may come in any order) and plans the work order over the GPU. Later calls with the same
-    tensor objects, unmodified,
-    reuse that (the reference memoises converted metadata on data_ptr() alone,
-    kernels/v7_blockptr_warpspec.py:167-176; here the key also holds the shapes, dtypes,
-    torch's in-place version counters and the tensor objects themselves). A CSR changed
+    tensor objects, unmodified, reuse that (the reference memoises converted metadata on
+    data_ptr() alone, kernels/v7_blockptr_warpspec.py:167-176; here the key also holds the
+    shapes, dtypes, torch's in-place version counters and the tensor objects themselves). A CSR changed
     outside torch (e.g. through a NumPy view of its memory) needs clear_csr_cache().
     USAGI_BSA_VALIDATE=0 (read at import) skips the check.
   * `setup` loads the ahead-of-time library first, so a missing build fails at setup time; like
