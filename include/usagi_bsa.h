@@ -15,9 +15,10 @@
  *   - row_ptr: int32 [B, H, T/128 + 1]; values are offsets local to each (b, h) row of col_idx
  *     (kernels/v7_blockptr_warpspec.py:77-80).
  *   - col_idx: int32 [B, H, max_nnz]; row qb lists key blocks in
- *     col_idx[b, h, row_ptr[qb] : row_ptr[qb+1]], ascending, with the diagonal (kb == qb) as the
- *     LAST entry. The diagonal is processed implicitly and causally masked; entries before it are
- *     processed unmasked (kernels/v7_blockptr_warpspec.py:83-136).
+ *     col_idx[b, h, row_ptr[qb] : row_ptr[qb+1]] with the diagonal (kb == qb) as the LAST entry
+ *     (the reference's rows are ascending; distinct blocks below qb in any order before the
+ *     diagonal give the same result). The diagonal is processed implicitly and causally masked;
+ *     entries before it are processed unmasked (kernels/v7_blockptr_warpspec.py:83-136).
  *   - seq_lens: int32 [B] or NULL (NULL: every sequence has length T). Query rows at or past
  *     seq_len get O = 0 and LSE = -inf (kernels/v7_blockptr_warpspec.py:63-67, 138-148).
  *   - lse: float32 [B, H, T], natural-log log-sum-exp of the scaled scores, or NULL to skip.

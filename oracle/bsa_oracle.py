@@ -7,8 +7,8 @@ Three restatements of the reference's math:
 
   dense_masked()  fp32 (or fp64) softmax attention over the dense token mask
                   block_mask(CSR) ∧ causal ∧ key < seq_len, rows t >= seq_len -> O = 0,
-                  LSE = -inf. This is the parity reference; for a valid CSR (ascending,
-                  diagonal last, all kb <= qb) it equals the reference's walk
+                  LSE = -inf. This is the parity reference; for a valid CSR (distinct
+                  blocks below qb, then the diagonal last) it equals the reference's walk
                   (kernels/v7_blockptr_warpspec.py:83-148).
   blockwise_v7()  the reference's own algorithm, step for step: per (b*h, qb) an online exp2
                   softmax over the off-diagonal CSR entries without a causal mask
