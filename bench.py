@@ -23,8 +23,10 @@ duration: the mean kernel duration over a second block of the same steps, right 
 ones, from events attached to each kernel dispatch itself; a call's latency adds a few us of
 launch gap and event packets to it) and, after that, burst_ms (back-to-back bursts);
 config.full_seq_variant (seq_lens None, the kernel with the length masks compiled out, against
-seq_lens of all T); config.analytic_rows (the analytic window path against the CSR path);
-config.reference_conditions (bf16 inputs, and bf16 with variable seq_lens, as the reference was
+seq_lens of all T); config.window_routing (the shim runs the window-shaped sliding and global
+CSRs on the analytic-row kernel: that against the CSR walk on the same tensors);
+config.csr_first_call (a call with CSR tensors the shim has not seen against a cached one, host
+wall time); config.reference_conditions (bf16 inputs, and bf16 with variable seq_lens, as the reference was
 scored); config.other_workloads (the long-context mixed workload, with and without the work
 plan); cpu_baseline (PyTorch CPU dense-masked attention on the host, median of 3, with the C
 walk beside it). profile.family_dispatches counts the kernel dispatches of the warmup and timed
@@ -49,8 +51,8 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
-from usagi_amd import _native  # noqa: E402
-from usagi_amd import block_sparse_attn_fwd, block_sparse_attn_fwd_window  # noqa: E402
+from usagi_amd import _native, submission  # noqa: E402
+from usagi_amd import block_sparse_attn_fwd  # noqa: E402
 from usagi_amd import patterns as P  # noqa: E402
 
 METRIC = "geomean fwd ms @B2 H16 T8192 D128 over 3 sparsity families; % fp16 MFMA peak"
@@ -512,20 +514,63 @@ def main() -> int:
                               "ratio_none_to_all_T": round(mn / mf, 4)}
         extra_cfg["full_seq_variant"] = full_seq
 
-        # Analytic rows (no CSR, block_sparse_attn_fwd_window) for the window-shaped families.
+        # Window-shaped CSRs: the shim runs them on the analytic-row kernel (no CSR reads); the
+        # CSR walk on the same tensors, straight through the C ABI, beside it.
         analytic = {}
         for name in P.FAMILIES:
-            ex = wl[name].extra
-            if "window" not in ex:
+            rp_d, ci_d = dev_csr[name]
+            route = submission._csr_entry(rp_d, ci_d, B, H, T // 128, dev, False).window
+            if route is None:
                 continue
-            t_w, t_c = time_calls([
-                lambda ex=ex: block_sparse_attn_fwd_window(q, k, v, ex["window"], ex["n_global"]),
-                lambda n=name: call(n)], args.steps, stream)
-            mw_, mc = float(np.median(t_w)), float(np.median(t_c))
-            analytic[name] = {"window": ex["window"], "n_global": ex["n_global"],
-                              "median_ms": round(mw_, 4), "csr_median_ms": round(mc, 4),
-                              "ratio_to_csr": round(mw_ / mc, 4)}
-        extra_cfg["analytic_rows"] = analytic
+            o_w = torch.empty_like(q)
+            l_w = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+
+            def csr_walk(rp_d=rp_d, ci_d=ci_d, o_w=o_w, l_w=l_w):
+                _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), rp_d.data_ptr(),
+                            ci_d.data_ptr(), None, o_w.data_ptr(), l_w.data_ptr(), B, H, T, D,
+                            ci_d.shape[-1], _native.FP16, None, 0, stream.cuda_stream)
+
+            t_s, t_c = time_calls([lambda n=name: call(n), csr_walk], args.steps, stream)
+            ms_, mc = float(np.median(t_s)), float(np.median(t_c))
+            analytic[name] = {"window": route[0], "n_global": route[1],
+                              "shim_median_ms": round(ms_, 4), "csr_walk_median_ms": round(mc, 4),
+                              "ratio_shim_to_csr_walk": round(ms_ / mc, 4)}
+        extra_cfg["window_routing"] = analytic
+
+        # A CSR the shim has not seen: the first call copies it to the host (a device
+        # synchronisation), checks its rows, looks for a window pattern and plans the work
+        # order. Timed end to end on the host (synchronised before and after) for fresh tensors
+        # holding the same CSR, against the same for a call whose CSR is cached.
+        first = {}
+        for name in P.FAMILIES:
+            rp_d, ci_d = dev_csr[name]
+            t_new, t_unchecked, t_hit = [], [], []
+            for _ in range(5):
+                for validate, ts_ in ((True, t_new), (False, t_unchecked)):
+                    submission.VALIDATE_CSR = validate
+                    fresh = (rp_d.clone(), ci_d.clone())
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    block_sparse_attn_fwd(q, k, v, fresh[0], fresh[1], None)
+                    torch.cuda.synchronize()
+                    ts_.append((time.perf_counter() - t0) * 1e3)
+                submission.VALIDATE_CSR = True
+                t0 = time.perf_counter()
+                call(name)
+                torch.cuda.synchronize()
+                t_hit.append((time.perf_counter() - t0) * 1e3)
+            first[name] = {"first_call_ms": round(float(np.median(t_new)), 4),
+                           "first_call_unchecked_ms": round(float(np.median(t_unchecked)), 4),
+                           "cached_call_ms": round(float(np.median(t_hit)), 4)}
+        submission.clear_csr_cache()
+        first["note"] = ("host wall time of one call, synchronised before and after, median of "
+                         "5: first_call_ms with freshly cloned CSR tensors (cache miss: host copy, "
+                         "check, window pattern and plan before the launch), "
+                         "first_call_unchecked_ms the same with USAGI_BSA_VALIDATE=0 (no check, no "
+                         "synchronisation: the CSR walk launches at once and the host copy "
+                         "follows it on the stream), cached_call_ms with the bench's own CSR "
+                         "tensors (cache hit)")
+        extra_cfg["csr_first_call"] = first
 
         # The reference was scored on bf16 inputs with variable sequence lengths
         # (docs/OPTIMIZATION_JOURNAL.md:14-16): the same three families that way.
@@ -537,6 +582,12 @@ def main() -> int:
             meds = {n: float(np.median(t)) for n, t in zip(P.FAMILIES, ts)}
             ref[label] = {"median_ms": {n: round(m, 4) for n, m in meds.items()},
                           "geomean_ms": round(geomean(list(meds.values())), 4)}
+            if sl is None:
+                ref[label]["frac_peak"] = {
+                    n: round(P.active_blocks(fams[n][0]) * FLOP_PER_BLOCK / m / 1e9
+                             / PEAK_FP16_TFLOPS, 4) for n, m in meds.items()}
+                ref[label]["ratio_to_fp16"] = round(
+                    ref[label]["geomean_ms"] / geomean(medians), 4)
         ref["note"] = ("bf16 q/k/v/O with fp16 P·V; the seq_lens line cuts batch 1 at "
                        f"{REF_SEQ_LENS[1]} tokens (the active-block FLOP count is not reduced)")
         extra_cfg["reference_conditions"] = ref

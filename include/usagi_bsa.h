@@ -92,14 +92,16 @@ int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
                          int32_t batch, int32_t heads, int32_t seq_len, int32_t head_dim,
                          int32_t dtype, void* stream);
 
-/* Host-side CSR validator over HOST copies of row_ptr / col_idx; no counterpart in the reference,
- * which does not validate its input (kernels/v7_blockptr_warpspec.py:155-191). It checks the
- * preconditions under which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-136
- * equals block-mask ∧ causal attention: row_ptr[0] == 0, every row non-empty and within
- * max_nnz, its last entry == qb, and the entries before it distinct and in [0, qb) (in any
- * order: the walk's result does not depend on it). Returns 0, or USAGI_BSA_ECSR with the first
- * offending (b, h, qb) in usagi_bsa_last_error(). */
-int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
+/* Host-side CSR validator over HOST copies of row_ptr / col_idx (and of seq_lens, int32 [B], or
+ * NULL for all T); no counterpart in the reference, which does not validate its input
+ * (kernels/v7_blockptr_warpspec.py:155-191). It checks the preconditions under which the
+ * implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-136 equals block-mask ∧ causal
+ * attention: row_ptr[0] == 0, every row non-empty and within max_nnz, its last entry == qb, and
+ * the entries before it distinct and in [0, qb) (in any order: the walk's result does not depend
+ * on it). Rows of query blocks starting at or past seq_len[b] are not checked: the walk never
+ * reads them (kernels/v7_blockptr_warpspec.py:63-67). Returns 0, or USAGI_BSA_ECSR with the
+ * first offending (b, h, qb) in usagi_bsa_last_error(). */
+int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx, const int32_t* seq_lens,
                         int32_t batch, int32_t heads, int32_t num_q_blocks, int32_t max_nnz);
 
 /* Work plan over a HOST copy of row_ptr; no counterpart in the reference, whose grid is
@@ -118,7 +120,8 @@ int usagi_bsa_plan(const int32_t* row_ptr, int32_t batch, int32_t heads, int32_t
  * and stop_event when it completes (hipExtLaunchKernel's events, attached to the dispatch
  * itself), so their elapsed time is the kernel's own duration, without the launch gap and event
  * packets that events recorded around the call include. hipEvent_t handles created with timing,
- * either may be NULL; the setting is consumed by that one launch. Returns 0. */
+ * either may be NULL. The setting is used up by the thread's next forward call, whether that call
+ * launches or rejects its arguments, so it never attaches to a later launch. Returns 0. */
 int usagi_bsa_time_next_launch(void* start_event, void* stop_event);
 
 /* Version string of this library, e.g. "usagi_bsa 0.2.0 gfx950". No counterpart in the

@@ -31,6 +31,26 @@ def run_gpu(q, k, v, rp, ci, sl=None):
     return o.float().cpu().numpy(), lse.cpu().numpy()
 
 
+def run_csr_walk(q, k, v, rp, ci, sl=None):
+    """The CSR walk straight through the C ABI (the shim would run a window-shaped CSR on the
+    analytic-row kernel instead)."""
+    from usagi_amd import _native
+
+    dq, dk, dv = (x.to(DEV) for x in (q, k, v))
+    B, H, T, D = dq.shape
+    drp = torch.from_numpy(np.ascontiguousarray(rp, dtype=np.int32)).to(DEV)
+    dci = torch.from_numpy(np.ascontiguousarray(ci, dtype=np.int32)).to(DEV)
+    dsl = None if sl is None else torch.as_tensor(np.asarray(sl, dtype=np.int32)).to(DEV)
+    o = torch.empty_like(dq)
+    lse = torch.empty((B, H, T), device=DEV, dtype=torch.float32)
+    _native.fwd(dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), drp.data_ptr(), dci.data_ptr(),
+                None if dsl is None else dsl.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H, T,
+                D, ci.shape[-1], _native.BF16 if dq.dtype == torch.bfloat16 else _native.FP16,
+                None, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), lse.cpu().numpy()
+
+
 def c_oracle(q, k, v, rp, ci, sl=None, generic=False):
     """The fp32 walk over every head (OpenMP), as float32 numpy (O, LSE)."""
     qs, ks, vs = (x.float().numpy() for x in (q, k, v))
@@ -389,10 +409,74 @@ def test_window_path_equals_csr_path_bitwise(B, H, T, w, g):
     rp, ci = P.global_csr(B, H, T, g, w) if g else P.sliding_csr(B, H, T, w)
     q, k, v = P.make_qkv(B, H, T, seed=41)
     print(f"case window w={w} g={g} B{B} H{H} T{T}", flush=True)
-    o_csr, lse_csr = run_gpu(q, k, v, rp, ci)
+    o_csr, lse_csr = run_csr_walk(q, k, v, rp, ci)
     o_win, lse_win = run_gpu_window(q, k, v, w, g)
     assert np.array_equal(o_win, o_csr)
     assert np.array_equal(lse_win, lse_csr)
+
+
+@pytest.mark.parametrize("name,pattern", [("sliding", (8, 0)), ("global", (4, 4))])
+def test_shim_routes_window_shaped_csr_to_the_analytic_rows(name, pattern):
+    """block_sparse_attn_fwd recognises a CSR that is exactly a window (+ global prefix)
+    pattern in its first-call check and runs the analytic-row kernel: bit-identical to the CSR
+    walk, and the cache entry records the pattern it took."""
+    from usagi_amd import submission
+
+    submission.clear_csr_cache()
+    w = P.workloads()[name]
+    rp, ci = w.csr()
+    q, k, v = P.make_qkv(w.B, w.H, w.T, seed=44)
+    print(f"case route {name}", flush=True)
+    dq, dk, dv = (x.to(DEV) for x in (q, k, v))
+    drp, dci = torch.from_numpy(rp).to(DEV), torch.from_numpy(ci).to(DEV)
+    o, lse = block_sparse_attn_fwd(dq, dk, dv, drp, dci, None)
+    torch.cuda.synchronize()
+    (entry,) = submission._csr_cache.values()
+    assert entry.window == pattern
+    o_csr, lse_csr = run_csr_walk(q, k, v, rp, ci)
+    assert np.array_equal(o.float().cpu().numpy(), o_csr)
+    assert np.array_equal(lse.cpu().numpy(), lse_csr)
+
+
+def test_shim_keeps_a_near_window_csr_on_the_csr_walk():
+    """A sliding CSR with one entry dropped is no longer the analytic pattern: the shim stays
+    on the CSR walk (bit-identical to it) and matches the fp32 walk of the altered rows."""
+    from usagi_amd import submission
+
+    submission.clear_csr_cache()
+    B, H, T = 2, 16, 8192
+    rows = lambda b, h, i: [x for x in P.sliding_row(i, 8) if not (b == 1 and h == 5 and i == 40 and x == 35)]  # noqa: E731,E501
+    rp, ci = P.make_csr(B, H, T, rows)
+    q, k, v = P.make_qkv(B, H, T, seed=45)
+    print("case route near-window", flush=True)
+    o, lse = run_gpu(q, k, v, rp, ci)
+    (entry,) = submission._csr_cache.values()
+    assert entry.window is None
+    o_csr, lse_csr = run_csr_walk(q, k, v, rp, ci)
+    assert np.array_equal(o, o_csr) and np.array_equal(lse, lse_csr)
+    oo, _ = c_oracle(q[1:, 5:6], k[1:, 5:6], v[1:, 5:6], rp[1:, 5:6], ci[1:, 5:6])
+    assert_close(o[1:, 5:6], oo)
+
+
+def test_rows_past_seq_len_may_hold_anything():
+    """The walk never reads the rows of query blocks at or past seq_len (v7:63-67), so the shim
+    accepts a CSR that leaves them empty when seq_lens is given; O = 0 and LSE = -inf there."""
+    from usagi_amd import submission
+
+    submission.clear_csr_cache()
+    B, H, T = 2, 2, 1024
+    sl = [1024, 300]
+    rp, ci = P.sliding_csr(B, H, T, 3)
+    rp[1, :, 4:] = rp[1, :, 3:4]  # batch 1: rows 3.. (query blocks from 384 on) left empty
+    q, k, v = P.make_qkv(B, H, T, seed=46)
+    print("case rows past seq_len", flush=True)
+    with pytest.raises(ValueError, match="empty"):
+        run_gpu(q, k, v, rp, ci)
+    o, lse = run_gpu(q, k, v, rp, ci, sl)
+    rp_ok, ci_ok = P.sliding_csr(B, H, T, 3)
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp_ok, ci_ok, np.array(sl))
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
 
 
 @pytest.mark.parametrize("seq_lens", [[1024, 700], [0, 1000], [128, 1]])

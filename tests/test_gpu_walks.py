@@ -241,3 +241,54 @@ def test_timing_hook_times_the_kernel_itself():
     call_ms = ev[0].elapsed_time(ev[3])
     assert 0.0 < kernel_ms <= call_ms, (kernel_ms, call_ms)
     assert torch.equal(o1, o2) and torch.equal(l1, l2) and torch.equal(o1, o3)
+
+
+def test_timing_hook_is_used_up_by_a_rejected_call():
+    """A forward call that rejects its arguments still uses up the events set before it, so they
+    never attach to a later, unrelated launch."""
+    w = P.workloads()["sliding"]
+    rp, ci = w.csr()
+    q, k, v = (x.to(DEV) for x in P.make_qkv(w.B, w.H, w.T, seed=18))
+    drp, dci = _dev(rp), _dev(ci)
+    st = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    for e in ev:
+        e.record(st)
+    torch.cuda.synchronize()
+    before = ev[0].elapsed_time(ev[1])
+    print("case timing hook after a rejected call", flush=True)
+    _native.time_next_launch(ev[0].cuda_event, ev[1].cuda_event)
+    with pytest.raises(_native.NativeError):
+        _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), drp.data_ptr(), dci.data_ptr(),
+                    None, q.data_ptr(), None, w.B, w.H, w.T, 64, ci.shape[-1], _native.FP16,
+                    None, 0, st.cuda_stream)  # head_dim 64: rejected before any launch
+    block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    torch.cuda.synchronize()
+    assert ev[0].elapsed_time(ev[1]) == before
+
+
+@pytest.mark.parametrize("name", ["mixed", "sliding"])
+def test_unchecked_csr_is_planned_without_a_synchronisation(monkeypatch, name):
+    """With the check off, the first call launches the CSR walk in the built-in order at once
+    and copies the CSR to the host behind it; a later call picks the copy up and switches to
+    the work plan (mixed) or the analytic rows (sliding). Every call gives the same bits."""
+    monkeypatch.setattr(submission, "VALIDATE_CSR", False)
+    submission.clear_csr_cache()
+    w = P.workloads()[name]
+    rp, ci = w.csr()
+    q, k, v = (x.to(DEV) for x in P.make_qkv(w.B, w.H, w.T, seed=19))
+    drp, dci = _dev(rp), _dev(ci)
+    print(f"case unchecked CSR {name}", flush=True)
+    o1, l1 = block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    (entry,) = submission._csr_cache.values()
+    assert entry.pending is not None and entry.sched is None and entry.window is None
+    torch.cuda.synchronize()
+    o2, l2 = block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    assert entry.pending is None
+    if name == "mixed":
+        assert entry.sched is not None and entry.n_slots > w.B * w.H * w.nqb
+    else:
+        assert entry.window == (8, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    submission.clear_csr_cache()

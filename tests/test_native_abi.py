@@ -112,7 +112,21 @@ def test_setup_on_cpu_device_returns_none_like_the_reference():
 
 def test_check_csr_null_and_sizes():
     lib = _native.load()
-    assert lib.usagi_bsa_check_csr(None, None, 1, 1, 1, 0) == -1
+    assert lib.usagi_bsa_check_csr(None, None, None, 1, 1, 1, 0) == -1
     rp = np.array([0, 1], np.int32)
     ci = np.array([0], np.int32)
-    assert lib.usagi_bsa_check_csr(rp.ctypes.data, ci.ctypes.data, 1, 1, 1, 1) == 0
+    assert lib.usagi_bsa_check_csr(rp.ctypes.data, ci.ctypes.data, None, 1, 1, 1, 1) == 0
+
+
+def test_setup_off_gpu_needs_no_library(monkeypatch, tmp_path):
+    """Like the reference (v7:202-203), setup returns None for a non-GPU device or no specs
+    without touching the library; on a GPU device a missing library is reported."""
+    class Spec:
+        t_max = 1024
+
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    assert usagi_amd.setup([Spec()], "cpu", usagi_amd.VARIANT_MANIFEST) is None
+    assert usagi_amd.setup([], "cuda", usagi_amd.VARIANT_MANIFEST) is None
+    with pytest.raises(RuntimeError, match="missing"):
+        usagi_amd.setup([Spec()], "cuda", usagi_amd.VARIANT_MANIFEST)

@@ -185,3 +185,94 @@ def test_cache_is_bounded():
         _cpu_entry(rp, ci)
     assert len(submission._csr_cache) == submission._CSR_CACHE_SIZE
     submission.clear_csr_cache()
+
+
+# ------------------------------------------------------------------------------ seq_lens, inference
+
+
+def test_rows_past_seq_len_are_not_checked():
+    """Rows of query blocks starting at or past seq_len are never read by the walk (v7:63-67),
+    so the C check, the Python validator and the shim's cache accept them in any state."""
+    submission.clear_csr_cache()
+    rp = np.array([[[0, 1, 3, 3, 3]]], np.int32)  # nqb = 4; rows 2 and 3 empty
+    ci = np.array([[[0, 0, 1]]], np.int32)
+    for sl in ([256], [129]):
+        _native.check_csr_host(rp, ci, 1, 1, 4, 3, seq_lens=np.array(sl, np.int32))
+        P.validate_csr(rp, ci, 512, seq_lens=sl)
+    for sl in (None, [257], [512]):
+        with pytest.raises(ValueError, match="empty"):
+            _native.check_csr_host(rp, ci, 1, 1, 4, 3,
+                                   seq_lens=None if sl is None else np.array(sl, np.int32))
+        with pytest.raises(ValueError, match="empty"):
+            P.validate_csr(rp, ci, 512, seq_lens=sl)
+    # no rows read at all: row_ptr may even start elsewhere
+    _native.check_csr_host(rp + 5, ci, 1, 1, 4, 3, seq_lens=np.array([0], np.int32))
+
+    trp, tci = torch.from_numpy(rp), torch.from_numpy(ci)
+    sl_t = torch.tensor([256], dtype=torch.int32)
+    e = submission._csr_entry(trp, tci, 1, 1, 4, torch.device("cpu"), False, sl_t)
+    assert submission._csr_entry(trp, tci, 1, 1, 4, torch.device("cpu"), False, sl_t) is e
+    with pytest.raises(ValueError, match="empty"):  # longer sequences read the empty rows
+        submission._csr_entry(trp, tci, 1, 1, 4, torch.device("cpu"), False, [512])
+    with pytest.raises(ValueError, match="empty"):
+        submission._csr_entry(trp, tci, 1, 1, 4, torch.device("cpu"), False, None)
+    assert submission._csr_entry(trp, tci, 1, 1, 4, torch.device("cpu"), False, [200]) is not e
+    submission.clear_csr_cache()
+
+
+def test_inference_mode_csr_is_cached():
+    """Inference tensors carry no version counter; their CSR is checked once and then reused."""
+    submission.clear_csr_cache()
+    with torch.inference_mode():
+        rp, ci = (torch.from_numpy(x).clone() for x in P.sliding_csr(1, 2, 512, 3))
+    assert rp.is_inference()
+    e = _cpu_entry(rp, ci)
+    assert _cpu_entry(rp, ci) is e
+    submission.clear_csr_cache()
+
+
+# ------------------------------------------------------------------------------ window patterns
+
+
+def _pattern(rp, ci):
+    return submission.window_pattern(rp.reshape(-1, rp.shape[-1]), ci.reshape(rp.shape[0] *
+                                     rp.shape[1], -1), rp.shape[-1] - 1)
+
+
+@pytest.mark.parametrize("name,want", [("plumbing", (4, 0)), ("sliding", (8, 0)),
+                                       ("global", (4, 4)), ("retrieval", None),
+                                       ("mixed", None)])
+def test_window_pattern_of_the_workloads(name, want):
+    rp, ci = P.workloads()[name].csr()
+    assert _pattern(rp, ci) == want
+
+
+@pytest.mark.parametrize("nqb", [1, 2, 5, 16, 64])
+@pytest.mark.parametrize("w", [1, 2, 3, 8, 70])
+@pytest.mark.parametrize("g", [0, 1, 4, 9])
+def test_window_pattern_reads_back_an_equivalent_pattern(nqb, w, g):
+    """Whatever (window, n_global) it reads off, the CSR of that pattern is the same arrays."""
+    T = 128 * nqb
+    rp, ci = P.global_csr(2, 3, T, g, w) if g else P.sliding_csr(2, 3, T, w)
+    got = _pattern(rp, ci)
+    assert got is not None
+    w2, g2 = got
+    rp2, ci2 = P.global_csr(2, 3, T, g2, w2) if g2 else P.sliding_csr(2, 3, T, w2)
+    assert np.array_equal(rp, rp2) and np.array_equal(ci, ci2[..., :ci.shape[-1]])
+
+
+def test_window_pattern_rejects_near_misses():
+    B, H, T = 2, 3, 2048
+    rp, ci = P.sliding_csr(B, H, T, 4)
+    assert _pattern(rp, ci) == (4, 0)
+    drop = lambda b, h, i: [x for x in P.sliding_row(i, 4) if not (h == 2 and i == 9 and x == 7)]  # noqa: E731,E501
+    assert _pattern(*P.make_csr(B, H, T, drop)) is None
+    other_head = lambda b, h, i: P.sliding_row(i, 5 if (b, h) == (1, 1) else 4)  # noqa: E731
+    assert _pattern(*P.make_csr(B, H, T, other_head)) is None
+    desc = lambda b, h, i: sorted(P.sliding_row(i, 4)[:-1], reverse=True) + [i]  # noqa: E731
+    assert _pattern(*P.make_csr(B, H, T, desc)) is None  # same blocks, another order
+    extra = lambda b, h, i: P.global_row(i, 1, 4) if i == 15 else P.sliding_row(i, 4)  # noqa: E731
+    assert _pattern(*P.make_csr(B, H, T, extra)) is None
+    # padding past the last row's end does not matter
+    ci_pad = np.concatenate([ci, np.full(ci.shape[:-1] + (5,), 77, np.int32)], axis=-1)
+    assert _pattern(rp, ci_pad) == (4, 0)

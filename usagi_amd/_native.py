@@ -56,7 +56,7 @@ def load() -> ctypes.CDLL:
     lib.usagi_bsa_fwd_generic.restype = ctypes.c_int
     lib.usagi_bsa_fwd_window.argtypes = [p, p, p, i32, i32, p, p, p, i32, i32, i32, i32, i32, p]
     lib.usagi_bsa_fwd_window.restype = ctypes.c_int
-    lib.usagi_bsa_check_csr.argtypes = [p, p, i32, i32, i32, i32]
+    lib.usagi_bsa_check_csr.argtypes = [p, p, p, i32, i32, i32, i32]
     lib.usagi_bsa_check_csr.restype = ctypes.c_int
     lib.usagi_bsa_plan.argtypes = [p, i32, i32, i32, i32, p, i32]
     lib.usagi_bsa_plan.restype = ctypes.c_int
@@ -126,13 +126,19 @@ def plan_host(row_ptr, batch: int, heads: int, nqb: int, generic: bool = False):
     return sched[:n].copy() if n else None
 
 
-def check_csr_host(row_ptr, col_idx, batch: int, heads: int, nqb: int, max_nnz: int) -> None:
-    """Validate host (numpy int32, C-contiguous) CSR arrays through the C validator."""
+def check_csr_host(row_ptr, col_idx, batch: int, heads: int, nqb: int, max_nnz: int,
+                   seq_lens=None) -> None:
+    """Validate host (numpy int32, C-contiguous) CSR arrays through the C validator; with
+    seq_lens (host, [batch]) the rows of query blocks at or past seq_len are not checked."""
     import numpy as np
 
     rp = np.ascontiguousarray(row_ptr, dtype=np.int32)
     ci = np.ascontiguousarray(col_idx, dtype=np.int32)
+    sl = None if seq_lens is None else np.ascontiguousarray(seq_lens, dtype=np.int32).reshape(-1)
+    if sl is not None and sl.size != batch:
+        raise ValueError(f"seq_lens must hold {batch} values, got {sl.size}")
     code = load().usagi_bsa_check_csr(rp.ctypes.data, ci.ctypes.data if ci.size else None,
+                                      None if sl is None else sl.ctypes.data,
                                       batch, heads, nqb, max_nnz)
     if code != 0:
         raise ValueError(f"malformed CSR: {last_error()}")

@@ -791,8 +791,21 @@ int prepare_csr(Args& a, const int32_t* row_ptr, const int32_t* col_idx, int32_t
 thread_local hipEvent_t g_next_start = nullptr;
 thread_local hipEvent_t g_next_stop = nullptr;
 
+struct LaunchEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+
+// Every forward entry point takes the pending events first, so the setting is used up by that
+// call whether it launches or rejects its arguments (it never carries over to a later launch).
+LaunchEvents take_events() {
+  LaunchEvents e{g_next_start, g_next_stop};
+  g_next_start = g_next_stop = nullptr;
+  return e;
+}
+
 template <bool kBf16, int kRows>
-int launch(const Args& a, int slots, hipStream_t s) {
+int launch(const Args& a, int slots, hipStream_t s, LaunchEvents ev) {
   const void* fn = a.seq_lens
                        ? reinterpret_cast<const void*>(&bsa_fwd_dma_kernel<kBf16, kRows, false>)
                        : reinterpret_cast<const void*>(&bsa_fwd_dma_kernel<kBf16, kRows, true>);
@@ -801,10 +814,9 @@ int launch(const Args& a, int slots, hipStream_t s) {
   // Both launch calls report this launch's own status (a prior error left on the thread by
   // another HIP call is neither taken for it nor cleared).
   hipError_t err;
-  if (g_next_start || g_next_stop) {
-    hipEvent_t e0 = g_next_start, e1 = g_next_stop;
-    g_next_start = g_next_stop = nullptr;
-    err = hipExtLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s, e0, e1, 0);
+  if (ev.start || ev.stop) {
+    err = hipExtLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s, ev.start,
+                             ev.stop, 0);
   } else {
     err = hipLaunchKernel(fn, dim3((unsigned)slots), dim3(kThreads), params, 0, s);
   }
@@ -813,10 +825,10 @@ int launch(const Args& a, int slots, hipStream_t s) {
 }
 
 template <int kRows>
-int launch_dtype(const Args& a, int32_t dtype, int slots, void* stream) {
+int launch_dtype(const Args& a, int32_t dtype, int slots, void* stream, LaunchEvents ev) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return dtype == USAGI_BSA_BF16 ? launch<true, kRows>(a, slots, s)
-                                 : launch<false, kRows>(a, slots, s);
+  return dtype == USAGI_BSA_BF16 ? launch<true, kRows>(a, slots, s, ev)
+                                 : launch<false, kRows>(a, slots, s, ev);
 }
 
 }  // namespace
@@ -835,11 +847,12 @@ extern "C" int usagi_bsa_fwd(const void* q, const void* k, const void* v,
                              int32_t dtype, const int32_t* sched, int32_t n_slots,
                              void* stream) {
   usagi_bsa_clear_error();
+  const LaunchEvents ev = take_events();
   Args a;
   int rc = prepare(a, q, k, v, seq_lens, out, lse, batch, heads, seq_len, head_dim, dtype);
   if (rc == USAGI_BSA_OK) rc = prepare_csr(a, row_ptr, col_idx, max_nnz, sched, n_slots);
   if (rc != USAGI_BSA_OK) return rc;
-  return launch_dtype<kRowsCsr>(a, dtype, sched ? n_slots : a.n_items, stream);
+  return launch_dtype<kRowsCsr>(a, dtype, sched ? n_slots : a.n_items, stream, ev);
 }
 
 extern "C" int usagi_bsa_fwd_generic(const void* q, const void* k, const void* v,
@@ -849,11 +862,12 @@ extern "C" int usagi_bsa_fwd_generic(const void* q, const void* k, const void* v
                                      int32_t head_dim, int32_t max_nnz, int32_t dtype,
                                      const int32_t* sched, int32_t n_slots, void* stream) {
   usagi_bsa_clear_error();
+  const LaunchEvents ev = take_events();
   Args a;
   int rc = prepare(a, q, k, v, seq_lens, out, lse, batch, heads, seq_len, head_dim, dtype);
   if (rc == USAGI_BSA_OK) rc = prepare_csr(a, row_ptr, col_idx, max_nnz, sched, n_slots);
   if (rc != USAGI_BSA_OK) return rc;
-  return launch_dtype<kRowsGeneric>(a, dtype, sched ? n_slots : a.n_items, stream);
+  return launch_dtype<kRowsGeneric>(a, dtype, sched ? n_slots : a.n_items, stream, ev);
 }
 
 extern "C" int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
@@ -862,6 +876,7 @@ extern "C" int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
                                     int32_t seq_len, int32_t head_dim, int32_t dtype,
                                     void* stream) {
   usagi_bsa_clear_error();
+  const LaunchEvents ev = take_events();
   Args a;
   const int rc = prepare(a, q, k, v, seq_lens, out, lse, batch, heads, seq_len, head_dim, dtype);
   if (rc != USAGI_BSA_OK) return rc;
@@ -869,5 +884,5 @@ extern "C" int usagi_bsa_fwd_window(const void* q, const void* k, const void* v,
   if (n_global < 0) return usagi_bsa_fail(USAGI_BSA_EINVAL, "n_global must be >= 0, got %d", (int)n_global);
   a.window = window;
   a.n_global = n_global;
-  return launch_dtype<kRowsWindow>(a, dtype, a.n_items, stream);
+  return launch_dtype<kRowsWindow>(a, dtype, a.n_items, stream, ev);
 }

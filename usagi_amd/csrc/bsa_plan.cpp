@@ -68,8 +68,9 @@ void usagi_bsa_clear_error(void) { g_err[0] = '\0'; }
 
 extern "C" const char* usagi_bsa_last_error(void) { return g_err; }
 
-extern "C" int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx, int32_t batch,
-                                   int32_t heads, int32_t num_q_blocks, int32_t max_nnz) {
+extern "C" int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_idx,
+                                   const int32_t* seq_lens, int32_t batch, int32_t heads,
+                                   int32_t num_q_blocks, int32_t max_nnz) {
   usagi_bsa_clear_error();
   if (!row_ptr || batch <= 0 || heads <= 0 || num_q_blocks <= 0 || max_nnz < 0 ||
       (max_nnz > 0 && !col_idx))
@@ -82,9 +83,19 @@ extern "C" int usagi_bsa_check_csr(const int32_t* row_ptr, const int32_t* col_id
     const int32_t* rp = row_ptr + bh * (num_q_blocks + 1);
     const int32_t* ci = col_idx ? col_idx + bh * (int64_t)max_nnz : nullptr;
     const int b = (int)(bh / heads), h = (int)(bh % heads);
-    if (rp[0] != 0)
+    // Rows of query blocks that start at or past seq_len are never read by the walk (their
+    // output is O = 0, LSE = -inf: kernels/v7_blockptr_warpspec.py:63-67), so they may hold
+    // anything; only the rows before them are checked.
+    int n_rows = num_q_blocks;
+    if (seq_lens) {
+      const int64_t sl = seq_lens[b];
+      n_rows = sl <= 0 ? 0
+                     : (int)std::min<int64_t>(num_q_blocks,
+                                              (sl + USAGI_BSA_BLOCK - 1) / USAGI_BSA_BLOCK);
+    }
+    if (n_rows > 0 && rp[0] != 0)
       return usagi_bsa_fail(USAGI_BSA_ECSR, "(b=%d,h=%d): row_ptr[0]=%d, expected 0", b, h, rp[0]);
-    for (int qb = 0; qb < num_q_blocks; ++qb, ++stamp) {
+    for (int qb = 0; qb < n_rows; ++qb, ++stamp) {
       const int rs = rp[qb], re = rp[qb + 1];
       if (re <= rs)
         return usagi_bsa_fail(USAGI_BSA_ECSR, "(b=%d,h=%d,qb=%d): empty or decreasing row (%d..%d)",

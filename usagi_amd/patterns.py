@@ -125,22 +125,28 @@ def active_blocks(row_ptr: np.ndarray) -> int:
     return int(row_ptr[..., -1].astype(np.int64).sum())
 
 
-def validate_csr(row_ptr: np.ndarray, col_idx: np.ndarray, T: int) -> None:
+def validate_csr(row_ptr: np.ndarray, col_idx: np.ndarray, T: int, seq_lens=None) -> None:
     """Raise ValueError unless every row is non-empty, ends with its diagonal, and lists the
     blocks before it at most once each, all in [0, qb) (any order): the precondition under
     which the implicit-diagonal walk of kernels/v7_blockptr_warpspec.py:83-136 equals
-    block-mask ∧ causal attention. Same rules as usagi_bsa_check_csr."""
+    block-mask ∧ causal attention. With seq_lens ([B]), rows of query blocks starting at or
+    past seq_len[b] are skipped: the walk never reads them (v7:63-67). Same rules as
+    usagi_bsa_check_csr."""
     B, H, n1 = row_ptr.shape
     nqb = T // BLOCK
     if n1 != nqb + 1:
         raise ValueError(f"row_ptr last dim {n1} != T/128 + 1 = {nqb + 1}")
     max_nnz = col_idx.shape[-1]
     for b in range(B):
+        n_rows = nqb
+        if seq_lens is not None:
+            sl = int(seq_lens[b])
+            n_rows = 0 if sl <= 0 else min(nqb, -(-sl // BLOCK))
         for h in range(H):
             rp = row_ptr[b, h]
-            if rp[0] != 0:
+            if n_rows and rp[0] != 0:
                 raise ValueError(f"(b={b},h={h}): row_ptr[0] = {rp[0]}")
-            for i in range(nqb):
+            for i in range(n_rows):
                 if rp[i + 1] <= rp[i]:
                     raise ValueError(f"(b={b},h={h},qb={i}): empty or decreasing row")
                 if rp[i + 1] > max_nnz:

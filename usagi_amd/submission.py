@@ -18,15 +18,24 @@ Differences from the reference, all deliberate:
     is empty, repeats a block, lists a block outside [0, qb) before its last entry, or does not
     end with its diagonal: the reference's walk, kernels/v7_blockptr_warpspec.py:83-111, would
     silently attend future tokens or count a block twice there; the entries before the diagonal
-    may come in any order) and plans the work order over the GPU. Later calls with the same
-    tensor objects, unmodified, reuse that (the reference memoises converted metadata on
+    may come in any order; rows of query blocks at or past seq_len, which the walk never reads
+    (v7:63-67), may hold anything) and plans the work order over the GPU. Later calls with the
+    same tensor objects, unmodified, reuse that (the reference memoises converted metadata on
     data_ptr() alone, kernels/v7_blockptr_warpspec.py:167-176; here the key also holds the
-    shapes, dtypes, torch's in-place version counters and the tensor objects themselves). A CSR changed
-    outside torch (e.g. through a NumPy view of its memory) needs clear_csr_cache().
-    USAGI_BSA_VALIDATE=0 (read at import) skips the check.
-  * `setup` loads the ahead-of-time library first, so a missing build fails at setup time; like
-    the reference it returns None without doing anything for a non-GPU device
-    (kernels/v7_blockptr_warpspec.py:202-203), and the entry points then reject CPU tensors
+    shapes, dtypes, torch's in-place version counters and the tensor objects themselves, and,
+    for a CSR that is only valid before seq_len, the seq_lens it was checked with). A CSR
+    changed outside torch (e.g. through a NumPy view of its memory), or an inference-mode CSR
+    changed in place (inference tensors have no version counter), needs clear_csr_cache().
+    USAGI_BSA_VALIDATE=0 (read at import) skips the check and with it the synchronisation: the
+    first call runs the CSR walk in the built-in order while a copy of the CSR goes to pinned
+    host memory behind it, and a later call, finding that copy done, plans the work order and
+    looks for a window pattern (like the reference, a malformed CSR then goes unreported).
+  * A CSR whose rows are exactly the analytic rows of a window or window + global-prefix
+    pattern (found by that same first-call check) runs the analytic-row kernel, which reads no
+    CSR and gives the same bits; USAGI_BSA_ROUTE_WINDOW=0 (read at import) turns that off.
+  * Like the reference, `setup` returns None without doing anything for a non-GPU device or
+    no specs (kernels/v7_blockptr_warpspec.py:202-203); on a GPU it loads the ahead-of-time
+    library first, so a missing build fails at setup time. The entry points reject CPU tensors
     (there is no CPU path).
 """
 
@@ -46,6 +55,10 @@ HEAD_DIM = 128
 VARIANT_MANIFEST = [{"name": "default"}]
 
 VALIDATE_CSR = os.environ.get("USAGI_BSA_VALIDATE", "1") not in ("", "0")
+# A CSR whose rows are exactly an analytic window / window + global-prefix pattern runs the
+# analytic-row kernel (no CSR reads, same result bit for bit); USAGI_BSA_ROUTE_WINDOW=0 (read
+# at import) keeps every call on the CSR walk.
+ROUTE_WINDOW = os.environ.get("USAGI_BSA_ROUTE_WINDOW", "1") not in ("", "0")
 
 _DTYPE_CODES = {torch.float16: _native.FP16, torch.bfloat16: _native.BF16}
 
@@ -54,15 +67,27 @@ _CSR_CACHE_SIZE = 64
 
 class _CsrEntry:
     """What the first call learnt about one (row_ptr, col_idx) pair: the tensors it was made
-    for (weak references) and the device copy of its work plan (None: built-in order)."""
+    for (weak references), the device copy of its work plan (None: built-in order) and the
+    stream that copy was made on, the analytic (window, n_global) pattern the rows spell out
+    (None: not one), and, when the rows are only valid before seq_len, the seq_lens they were
+    checked with (seq_key; None: every row is valid)."""
 
-    __slots__ = ("row_ptr", "col_idx", "sched", "n_slots")
+    __slots__ = ("row_ptr", "col_idx", "sched", "n_slots", "stream", "window", "seq_key",
+                 "seq_ref", "pending", "sched_host")
 
-    def __init__(self, row_ptr, col_idx, sched, n_slots):
+    def __init__(self, row_ptr, col_idx, sched, n_slots, stream, window, seq_key, seq_ref):
         self.row_ptr = weakref.ref(row_ptr)
         self.col_idx = weakref.ref(col_idx)
         self.sched = sched
         self.n_slots = n_slots
+        self.stream = stream
+        self.window = window
+        self.seq_key = seq_key
+        self.seq_ref = seq_ref
+        # Unchecked CSRs (USAGI_BSA_VALIDATE=0): (event, pinned row_ptr, pinned col_idx, B, H,
+        # nqb) of the host copy still in flight, or None.
+        self.pending = None
+        self.sched_host = None
 
 
 _csr_cache: "OrderedDict[tuple, _CsrEntry]" = OrderedDict()
@@ -74,27 +99,134 @@ def clear_csr_cache() -> None:
 
 
 def _tensor_key(t: torch.Tensor) -> tuple:
-    return (t.device, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, t._version)
+    # Inference tensors have no version counter: an in-place change to one made in inference
+    # mode is not seen (like a change made outside torch, it needs clear_csr_cache()).
+    version = None if t.is_inference() else t._version
+    return (t.device, t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype, version)
 
 
-def _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic: bool) -> _CsrEntry:
+def _seq_key(seq_lens):
+    """Cache key of a seq_lens argument and the tensor to hold a weak reference to (or None)."""
+    if seq_lens is None:
+        return None, None
+    if isinstance(seq_lens, torch.Tensor):
+        return ("tensor",) + _tensor_key(seq_lens), seq_lens
+    return ("values", tuple(int(x) for x in seq_lens)), None
+
+
+def window_pattern(rp, ci, nqb: int):
+    """(window, n_global) when every (b, h) row of the host CSR (rp [BH, nqb+1], ci [BH,
+    max_nnz]) is exactly the analytic row of that pattern: query block i attends blocks
+    0 .. n_global-1 and max(0, i-window+1) .. i, deduplicated and ascending (the rows of the
+    reference's _fwd_window / _fwd_window_global, kernels/v1_baseline.py:141-322); else None.
+    The pattern is read off the last row (a run of consecutive blocks ending at the diagonal,
+    after a prefix 0 .. g-1), then every row of every head is compared with it."""
+    import numpy as np
+
+    rp = np.asarray(rp).reshape(-1, nqb + 1)
+    ci = np.asarray(ci).reshape(rp.shape[0], -1)
+    last = nqb - 1
+    rs, re = int(rp[0, last]), int(rp[0, nqb])
+    if not (0 <= rs < re <= ci.shape[1]):
+        return None
+    row = ci[0, rs:re]
+    n = len(row)
+    if row[-1] != last:
+        return None
+    run = 1
+    while run < n and row[n - 1 - run] == last - run:
+        run += 1
+    g = n - run
+    if g and not np.array_equal(row[:g], np.arange(g)):
+        return None
+    window, n_global = run, g
+    q = np.arange(nqb)
+    lo = np.maximum(q - window + 1, 0)
+    ng = np.minimum(n_global, lo)
+    counts = ng + (q - lo + 1)
+    exp_rp = np.concatenate(([0], np.cumsum(counts)))
+    nnz = int(exp_rp[-1])
+    if nnz > ci.shape[1] or not np.array_equal(rp, np.broadcast_to(exp_rp, rp.shape)):
+        return None
+    # Entry p of row i: p itself in the global prefix (p < ng[i]), else lo[i] + (p - ng[i]).
+    row_of = np.repeat(q, counts)
+    p = np.arange(nnz) - np.repeat(exp_rp[:-1], counts)
+    ng_r = ng[row_of]
+    exp_ci = np.where(p < ng_r, p, lo[row_of] + (p - ng_r))
+    if not np.array_equal(ci[:, :nnz], np.broadcast_to(exp_ci, (ci.shape[0], nnz))):
+        return None
+    return window, n_global
+
+
+def _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic: bool, seq_lens=None) -> _CsrEntry:
     key = (generic, dev, _tensor_key(row_ptr), _tensor_key(col_idx))
     e = _csr_cache.get(key)
     if e is not None and e.row_ptr() is row_ptr and e.col_idx() is col_idx:
-        _csr_cache.move_to_end(key)
-        return e
-    rp = row_ptr.detach().reshape(B, H, nqb + 1).to("cpu", torch.int32).contiguous().numpy()
+        if e.seq_key is None or (_seq_key(seq_lens)[0] == e.seq_key and
+                                 (e.seq_ref is None or e.seq_ref() is seq_lens)):
+            _csr_cache.move_to_end(key)
+            if e.pending is not None and e.pending[0].query():
+                _finish_pending(e, dev, generic)
+            return e
     max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
-    ci = col_idx.detach().reshape(B, H, max_nnz).to("cpu", torch.int32).contiguous().numpy()
-    if not generic and VALIDATE_CSR:
-        _native.check_csr_host(rp, ci, B, H, nqb, max_nnz)
-    sched = _native.plan_host(rp, B, H, nqb, generic)
-    dsched = torch.from_numpy(sched).to(dev) if sched is not None else None
-    e = _CsrEntry(row_ptr, col_idx, dsched, 0 if sched is None else len(sched))
+    stream = torch.cuda.current_stream(dev) if dev.type == "cuda" else None
+    if not VALIDATE_CSR and dev.type == "cuda":
+        # No check, so nothing has to be known before this launch: it runs the CSR walk in the
+        # built-in order while a copy of the CSR goes to pinned host memory behind it on the
+        # stream; a later call finds the copy done (an event query, no synchronisation) and
+        # plans the work order and looks for a window pattern then.
+        rp_h = torch.empty((B, H, nqb + 1), dtype=torch.int32, pin_memory=True)
+        ci_h = torch.empty((B, H, max_nnz), dtype=torch.int32, pin_memory=True)
+        rp_h.copy_(_as_int32_device(row_ptr, dev, (B, H, nqb + 1)), non_blocking=True)
+        ci_h.copy_(_as_int32_device(col_idx, dev, (B, H, max_nnz)), non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(stream)
+        e = _CsrEntry(row_ptr, col_idx, None, 0, stream, None, None, None)
+        e.pending = (done, rp_h, ci_h, B, H, nqb)
+    else:
+        rp = row_ptr.detach().reshape(B, H, nqb + 1).to("cpu", torch.int32).contiguous().numpy()
+        ci = col_idx.detach().reshape(B, H, max_nnz).to("cpu", torch.int32).contiguous().numpy()
+        seq_key = seq_ref = None
+        if not generic and VALIDATE_CSR:
+            try:
+                _native.check_csr_host(rp, ci, B, H, nqb, max_nnz)
+            except ValueError:
+                # Rows past seq_len are never read, so they may hold anything: check the rest.
+                if seq_lens is None:
+                    raise
+                sl = torch.as_tensor(seq_lens).detach().to("cpu", torch.int32).reshape(-1).numpy()
+                _native.check_csr_host(rp, ci, B, H, nqb, max_nnz, seq_lens=sl)
+                seq_key, sref = _seq_key(seq_lens)
+                seq_ref = None if sref is None else weakref.ref(sref)
+        e = _CsrEntry(row_ptr, col_idx, None, 0, stream, None, seq_key, seq_ref)
+        _plan_entry(e, rp, ci, B, H, nqb, dev, generic)
     _csr_cache[key] = e
     while len(_csr_cache) > _CSR_CACHE_SIZE:
         _csr_cache.popitem(last=False)
     return e
+
+
+def _plan_entry(e: _CsrEntry, rp, ci, B, H, nqb, dev, generic: bool, pinned=False) -> None:
+    """Work plan and window pattern of a host copy of the CSR, into the entry."""
+    window = None
+    if not generic and ROUTE_WINDOW and ci.shape[-1]:
+        window = window_pattern(rp, ci, nqb)
+    sched = _native.plan_host(rp, B, H, nqb, generic)
+    if sched is not None:
+        src = torch.from_numpy(sched)
+        if pinned:  # copied behind the stream's queued work, no synchronisation
+            src = src.pin_memory()
+            e.sched_host = src  # stays alive until the copy has run
+        e.sched = src.to(dev, non_blocking=pinned)
+        e.n_slots = len(sched)
+        e.stream = torch.cuda.current_stream(dev) if dev.type == "cuda" else None
+    e.window = window if sched is None else None
+
+
+def _finish_pending(e: _CsrEntry, dev, generic: bool) -> None:
+    _, rp_h, ci_h, B, H, nqb = e.pending
+    e.pending = None
+    _plan_entry(e, rp_h.numpy(), ci_h.numpy(), B, H, nqb, dev, generic, pinned=True)
 
 
 def _as_int32_device(t: torch.Tensor, device: torch.device, shape: tuple) -> torch.Tensor:
@@ -140,25 +272,34 @@ def _run_csr(q, k, v, row_ptr, col_idx, seq_lens, generic: bool):
     max_nnz = col_idx.shape[-1] if col_idx.dim() else 0
     if col_idx.numel() != B * H * max_nnz:
         raise ValueError(f"col_idx must be [B, H, max_nnz], got shape {tuple(col_idx.shape)}")
-    plan = _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic)
+    plan = _csr_entry(row_ptr, col_idx, B, H, nqb, dev, generic, seq_lens)
     q = q.contiguous()
     k = k.contiguous()
     v = v.contiguous()
-    rp = _as_int32_device(row_ptr, dev, (B, H, nqb + 1))
-    ci = _as_int32_device(col_idx, dev, (B, H, max_nnz))
     sl = None
     if seq_lens is not None:
         sl = _as_int32_device(torch.as_tensor(seq_lens), dev, (B,))
-
     out = torch.empty((B, H, T, D), device=dev, dtype=q.dtype)
     lse = torch.empty((B, H, T), device=dev, dtype=torch.float32)
     with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = torch.cuda.current_stream(dev)
+        if plan.window is not None:
+            _native.fwd_window(q.data_ptr(), k.data_ptr(), v.data_ptr(), plan.window[0],
+                               plan.window[1], sl.data_ptr() if sl is not None else None,
+                               out.data_ptr(), lse.data_ptr(), B, H, T, D,
+                               _DTYPE_CODES[q.dtype], stream.cuda_stream)
+            return out, lse
+        rp = _as_int32_device(row_ptr, dev, (B, H, nqb + 1))
+        ci = _as_int32_device(col_idx, dev, (B, H, max_nnz))
+        if plan.sched is not None and stream != plan.stream:
+            # The plan's memory belongs to the stream it was copied on; a launch on another
+            # stream must keep it from being reused while the kernel reads it.
+            plan.sched.record_stream(stream)
         _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), rp.data_ptr(),
                     ci.data_ptr() if max_nnz else None, sl.data_ptr() if sl is not None else None,
                     out.data_ptr(), lse.data_ptr(), B, H, T, D, max_nnz, _DTYPE_CODES[q.dtype],
                     plan.sched.data_ptr() if plan.sched is not None else None, plan.n_slots,
-                    stream, generic=generic)
+                    stream.cuda_stream, generic=generic)
     return out, lse
 
 
@@ -214,14 +355,15 @@ def block_sparse_attn_fwd_window(q, k, v, window, n_global=0, seq_lens=None):
 def setup(suite_specs, device, variants):
     """Load the ahead-of-time library and run one tiny launch per distinct T.
 
-    Mirrors kernels/v7_blockptr_warpspec.py:201-247 (a diagonal-only CSR per spec, then a
-    synchronise). Specs only need a `t_max` attribute.
+    Mirrors kernels/v7_blockptr_warpspec.py:201-247: None without doing anything for a non-GPU
+    device or no specs (v7:202-203), else a diagonal-only CSR launch per spec, then a
+    synchronise. Specs only need a `t_max` attribute.
     """
-    _native.load()
     if str(device) != "cuda" and not str(device).startswith("cuda:"):
         return None
     if not suite_specs:
         return None
+    _native.load()
     dev = torch.device(device)
     seen = set()
     for spec in suite_specs:
