@@ -30,7 +30,8 @@ wall time); config.reference_conditions (bf16 inputs, and bf16 with variable seq
 scored); config.other_workloads (the long-context mixed workload, with and without the work
 plan); cpu_baseline (PyTorch CPU dense-masked attention on the host, median of 3, with the C
 walk beside it). profile.family_dispatches counts the kernel dispatches of the warmup and timed
-steps, which --pmc-summary attributes to the families when given the JSON of a profiled run.
+steps, which --pmc-summary and --trace-summary attribute to the families when given the JSON of
+a profiled run.
 """
 
 from __future__ import annotations
@@ -303,6 +304,54 @@ def pmc_summary(paths, calib_mib: int, bench_json) -> int:
     return 0
 
 
+def trace_summary(trace_csv: str, bench_json: str) -> int:
+    """Per-family kernel durations from a rocprofv3 --kernel-trace of a run of this script.
+
+    The kernel's dispatches are taken in order: the first profile.family_dispatches are the
+    warmup and timed steps (family FAMILIES[i % 3] for dispatch i), the timed ones being the last
+    3 x steps of them; the next profile.kernel_timing_dispatches repeat the timed steps with
+    events attached to each dispatch (the launch_ms of the JSON line). Prints both blocks beside
+    the JSON line's figures."""
+    import csv
+
+    with open(bench_json) as f:
+        line = [x for x in f.read().splitlines() if x.startswith("{")][-1]
+    bj = json.loads(line)
+    n_fam = int(bj["profile"]["family_dispatches"])
+    n_kt = int(bj["profile"]["kernel_timing_dispatches"])
+    steps = int(bj["steps"])
+    fams = bj["config"]["families"]
+    with open(trace_csv) as f:
+        rows = [r for r in csv.DictReader(f) if KERNEL in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    if len(rows) < n_fam + n_kt:
+        print(f"{trace_csv}: {len(rows)} kernel dispatches, fewer than {n_fam + n_kt}", file=sys.stderr)
+        return 2
+    dur = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
+    nf = len(FAM_ORDER)
+    blocks = (("timed per-call dispatches", n_fam - nf * steps, n_fam, "median_ms",
+               "call latency"),
+              ("kernel-timing dispatches (events attached to each dispatch)", n_fam,
+               n_fam + n_kt, "launch_ms", "launch_ms"))
+    for title, lo, hi, key, what in blocks:
+        print(f"## {title}: kernel dispatches {lo} .. {hi - 1} of the run, ns")
+        means = []
+        for fi, fam in enumerate(FAM_ORDER):
+            d = np.array([dur[i] for i in range(lo, hi) if (i - lo) % nf == fi])
+            means.append(d.mean())
+            ref = fams[fam][key] * 1e6
+            print(f"{fam:10s} n={len(d)} mean={d.mean():.0f} median={np.median(d):.0f} "
+                  f"min={d.min()} max={d.max()}   bench {key} {ref:.0f} ({what} "
+                  f"{ref - np.median(d):+.0f} ns over the kernel's median)")
+        print(f"all three  mean of family means {np.mean(means):.0f}")
+    names = sorted({r["Kernel_Name"] for r in rows[:n_fam]})
+    print("kernels of the timed steps: " + "; ".join(names))
+    return 0
+
+
+FAM_ORDER = P.FAMILIES
+
+
 def event_pair():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -362,11 +411,20 @@ def main() -> int:
                     help="summarise rocprofv3 --pmc counter_collection.csv files of a run of "
                          "this script (made with --calib-copy-mib) and exit; no GPU is used")
     ap.add_argument("--bench-json", nargs="+",
-                    help="with --pmc-summary: the JSON output of each profiled run")
+                    help="with --pmc-summary / --trace-summary: the JSON output of each "
+                         "profiled run")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise the run_kernel_trace.csv of a rocprofv3 --kernel-trace run of "
+                         "this script per family (needs --bench-json) and exit; no GPU is used")
     args = ap.parse_args()
 
     if args.pmc_summary:
         return pmc_summary(args.pmc_summary, args.calib_copy_mib, args.bench_json)
+    if args.trace_summary:
+        if not args.bench_json:
+            print("--trace-summary needs --bench-json", file=sys.stderr)
+            return 2
+        return trace_summary(args.trace_summary, args.bench_json[0])
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path has no multi-GPU mode "

@@ -151,3 +151,49 @@ def test_more_than_one_gpu_exits_with_a_message():
                          capture_output=True, text=True, timeout=300)
     assert out.returncode == 2
     assert "one GPU" in out.stderr and not out.stdout.strip()
+
+
+def test_trace_summary_splits_timed_and_kernel_timing_dispatches(tmp_path):
+    """bench.py --trace-summary: 2 warmup + 3 timed steps, then 3 kernel-timing steps, then
+    dispatches that must be left out. Family f's timed dispatches last 100 + 10 f us (step 0, 1:
+    far off), its kernel-timing ones 200 + 10 f us."""
+    steps, warm = 3, 2
+    trace = [(1, "__amd_rocclr_copyBuffer", 0, 5)]
+    d = 2
+    for s in range(warm + steps + steps):
+        for fi, _ in enumerate(P.FAMILIES):
+            if s < warm:
+                us = 999
+            elif s < warm + steps:
+                us = 100 + 10 * fi
+            else:
+                us = 200 + 10 * fi
+            trace.append((d, KERNEL, 1_000_000_000 * d, 1_000_000_000 * d + us * 1000))
+            d += 1
+    for _ in range(5):
+        trace.append((d, KERNEL, 1_000_000_000 * d, 1_000_000_000 * d + 7))
+        d += 1
+    csv_path = os.path.join(str(tmp_path), "run_kernel_trace.csv")
+    with open(csv_path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(["Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"])
+        w.writerows(trace)
+    fams = {fam: {"median_ms": (105 + 10 * fi) / 1e3, "launch_ms": (200 + 10 * fi) / 1e3}
+            for fi, fam in enumerate(P.FAMILIES)}
+    bj = os.path.join(str(tmp_path), "bench.json")
+    with open(bj, "w") as f:
+        f.write(json.dumps({"steps": steps, "config": {"families": fams},
+                            "profile": {"family_dispatches": 3 * (warm + steps),
+                                        "kernel_timing_dispatches": 3 * steps}}) + "\n")
+    out = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--trace-summary",
+                          csv_path, "--bench-json", bj], capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    blocks = out.stdout.split("## ")[1:]
+    assert len(blocks) == 2
+    for block, base in zip(blocks, (100, 200)):
+        for fi, fam in enumerate(P.FAMILIES):
+            line = next(l for l in block.splitlines() if l.startswith(fam))
+            assert f"n={steps} " in line and f"median={(base + 10 * fi) * 1000} " in line, line
+    assert "(call latency +5000 ns" in blocks[0]
+    assert "mean of family means 210000" in blocks[1]
