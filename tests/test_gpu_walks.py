@@ -292,3 +292,30 @@ def test_unchecked_csr_is_planned_without_a_synchronisation(monkeypatch, name):
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     submission.clear_csr_cache()
+
+
+@pytest.mark.parametrize("validate", [True, False])
+def test_planned_csr_launched_from_other_streams(monkeypatch, validate):
+    """A work plan copied on one stream is used by launches on others (they wait for an
+    asynchronous copy and keep its memory alive): every stream gives the same bits."""
+    monkeypatch.setattr(submission, "VALIDATE_CSR", validate)
+    submission.clear_csr_cache()
+    w = P.workloads()["mixed"]
+    rp, ci = w.csr()
+    q, k, v = (x.to(DEV) for x in P.make_qkv(w.B, w.H, w.T, seed=20))
+    drp, dci = _dev(rp), _dev(ci)
+    print(f"case plan across streams validate={validate}", flush=True)
+    o0, l0 = block_sparse_attn_fwd(q, k, v, drp, dci, None)
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(2):
+        s2 = torch.cuda.Stream()
+        with torch.cuda.stream(s2):
+            outs.append(block_sparse_attn_fwd(q, k, v, drp, dci, None))
+        outs.append(block_sparse_attn_fwd(q, k, v, drp, dci, None))
+    torch.cuda.synchronize()
+    (entry,) = submission._csr_cache.values()
+    assert entry.sched is not None and entry.pending is None
+    for o, l in outs:
+        assert torch.equal(o, o0) and torch.equal(l, l0)
+    submission.clear_csr_cache()

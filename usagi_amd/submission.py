@@ -73,7 +73,7 @@ class _CsrEntry:
     checked with (seq_key; None: every row is valid)."""
 
     __slots__ = ("row_ptr", "col_idx", "sched", "n_slots", "stream", "window", "seq_key",
-                 "seq_ref", "pending", "sched_host")
+                 "seq_ref", "pending", "sched_host", "sched_ready")
 
     def __init__(self, row_ptr, col_idx, sched, n_slots, stream, window, seq_key, seq_ref):
         self.row_ptr = weakref.ref(row_ptr)
@@ -88,6 +88,9 @@ class _CsrEntry:
         # nqb) of the host copy still in flight, or None.
         self.pending = None
         self.sched_host = None
+        # Event after an asynchronous copy of the plan to the device (or None: the copy was
+        # synchronous); a launch on another stream waits for it.
+        self.sched_ready = None
 
 
 _csr_cache: "OrderedDict[tuple, _CsrEntry]" = OrderedDict()
@@ -220,6 +223,9 @@ def _plan_entry(e: _CsrEntry, rp, ci, B, H, nqb, dev, generic: bool, pinned=Fals
         e.sched = src.to(dev, non_blocking=pinned)
         e.n_slots = len(sched)
         e.stream = torch.cuda.current_stream(dev) if dev.type == "cuda" else None
+        if pinned:
+            e.sched_ready = torch.cuda.Event()
+            e.sched_ready.record(e.stream)
     e.window = window if sched is None else None
 
 
@@ -293,7 +299,10 @@ def _run_csr(q, k, v, row_ptr, col_idx, seq_lens, generic: bool):
         ci = _as_int32_device(col_idx, dev, (B, H, max_nnz))
         if plan.sched is not None and stream != plan.stream:
             # The plan's memory belongs to the stream it was copied on; a launch on another
-            # stream must keep it from being reused while the kernel reads it.
+            # stream waits for an asynchronous copy to land and keeps the memory from being
+            # reused while the kernel reads it.
+            if plan.sched_ready is not None:
+                stream.wait_event(plan.sched_ready)
             plan.sched.record_stream(stream)
         _native.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), rp.data_ptr(),
                     ci.data_ptr() if max_nnz else None, sl.data_ptr() if sl is not None else None,
