@@ -605,14 +605,16 @@ def main() -> int:
             t_new, t_unchecked, t_hit = [], [], []
             for _ in range(5):
                 for validate, ts_ in ((True, t_new), (False, t_unchecked)):
-                    submission.VALIDATE_CSR = validate
                     fresh = (rp_d.clone(), ci_d.clone())
                     torch.cuda.synchronize()
-                    t0 = time.perf_counter()
-                    block_sparse_attn_fwd(q, k, v, fresh[0], fresh[1], None)
-                    torch.cuda.synchronize()
-                    ts_.append((time.perf_counter() - t0) * 1e3)
-                submission.VALIDATE_CSR = True
+                    submission.VALIDATE_CSR = validate
+                    try:
+                        t0 = time.perf_counter()
+                        block_sparse_attn_fwd(q, k, v, fresh[0], fresh[1], None)
+                        torch.cuda.synchronize()
+                        ts_.append((time.perf_counter() - t0) * 1e3)
+                    finally:
+                        submission.VALIDATE_CSR = True
                 t0 = time.perf_counter()
                 call(name)
                 torch.cuda.synchronize()
