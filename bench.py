@@ -28,7 +28,9 @@ CSRs on the analytic-row kernel: that against the CSR walk on the same tensors);
 config.csr_first_call (a call with CSR tensors the shim has not seen against a cached one, host
 wall time); config.reference_conditions (bf16 inputs, and bf16 with variable seq_lens, as the reference was
 scored); config.other_workloads (the long-context mixed workload, with and without the work
-plan); cpu_baseline (PyTorch CPU dense-masked attention on the host, median of 3, with the C
+plan; sliding w2, whose short rows run the pipelined kernel, against the two-phase kernel);
+config.power_context (the sliding family on all-zero inputs, which keep the part at its top
+clock, and a dense fp16 GEMM on random inputs on the same box); cpu_baseline (PyTorch CPU dense-masked attention on the host, median of 3, with the C
 walk beside it). profile.family_dispatches counts the kernel dispatches of the warmup and timed
 steps, which --pmc-summary and --trace-summary attribute to the families when given the JSON of
 a profiled run.
@@ -455,6 +457,13 @@ def main() -> int:
         mrp, mci = mw.csr()
         mixed = (mq, mk, mv, mrp, torch.from_numpy(mrp).to(dev), torch.from_numpy(mci).to(dev))
         qb16, kb16, vb16 = (x.to(torch.bfloat16) for x in (q, k, v))
+        srp, sci = P.sliding_csr(B, H, T, 2)
+        srpd, scid = (torch.from_numpy(x).to(dev) for x in (srp, sci))
+        qz, kz, vz = (torch.zeros_like(x) for x in (q, k, v))
+        gen = torch.Generator(device=dev).manual_seed(args.seed)
+        ga = torch.randn((8192, 8192), device=dev, dtype=torch.float16, generator=gen)
+        gb = torch.randn((8192, 8192), device=dev, dtype=torch.float16, generator=gen)
+        gc = torch.empty((8192, 8192), device=dev, dtype=torch.float16)
     full_sl = torch.full((B,), T, dtype=torch.int32, device=dev)
     ref_sl = torch.tensor(REF_SEQ_LENS, dtype=torch.int32, device=dev)
 
@@ -679,6 +688,51 @@ def main() -> int:
             "builtin_order_median_ms": round(mb, 4),
             "ratio_plan_to_builtin": round(mp / mb, 4)}}
         del mixed, mq, mk, mv
+
+        # Short rows (sliding w2 on the same tensors): the pipelined kernel, which the library
+        # picks for rows of at most 4 blocks, against the two-phase kernel on the same calls.
+        sfn = [lambda: block_sparse_attn_fwd(q, k, v, srpd, scid, None)]
+        short = {}
+        prev = os.environ.get("USAGI_BSA_PIPE")
+        try:
+            for label, mode in (("pipelined", "1"), ("two_phase", "0")):
+                os.environ["USAGI_BSA_PIPE"] = mode
+                warm(sfn, args.min_warmup_s)
+                short[label] = float(np.median(time_calls(sfn, args.steps, stream)[0]))
+        finally:
+            if prev is None:
+                os.environ.pop("USAGI_BSA_PIPE", None)
+            else:
+                os.environ["USAGI_BSA_PIPE"] = prev
+        sfl = P.active_blocks(srp) * FLOP_PER_BLOCK
+        extra_cfg["other_workloads"]["sliding_w2"] = {
+            "B": B, "H": H, "T": T, "active_blocks": P.active_blocks(srp),
+            "median_ms": round(short["pipelined"], 4),
+            "frac_peak": round(sfl / short["pipelined"] / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "two_phase_kernel_median_ms": round(short["two_phase"], 4),
+            "ratio_pipelined_to_two_phase": round(short["pipelined"] / short["two_phase"], 4)}
+
+        # Power context: the sliding family on all-zero inputs (no operand bits toggle, the part
+        # keeps its top clock), and a dense fp16 GEMM on random inputs (torch.matmul, 8192^3),
+        # both on this box right after the timed steps.
+        zfn = [lambda: block_sparse_attn_fwd(qz, kz, vz, *dev_csr["sliding"], None)]
+        warm(zfn, args.min_warmup_s)
+        zero_ms = float(np.median(time_calls(zfn, args.steps, stream)[0]))
+        del qz, kz, vz
+        gfn = [lambda: torch.matmul(ga, gb, out=gc)]
+        warm(gfn, args.min_warmup_s)
+        gemm_ms = float(np.median(time_calls(gfn, args.steps, stream)[0]))
+        gemm_tflops = 2.0 * 8192 ** 3 / gemm_ms / 1e9
+        del ga, gb, gc
+        extra_cfg["power_context"] = {
+            "sliding_zero_inputs_ms": round(zero_ms, 4),
+            "sliding_random_inputs_ms": round(fam_out["sliding"]["median_ms"], 4),
+            "ratio_random_to_zero": round(fam_out["sliding"]["median_ms"] / zero_ms, 4),
+            "dense_fp16_gemm_tflops": round(gemm_tflops, 1),
+            "dense_fp16_gemm_frac_peak": round(gemm_tflops / PEAK_FP16_TFLOPS, 4),
+            "note": ("call medians on the same box after the timed steps; all-zero inputs keep "
+                     "the part at its top clock, random fp16 inputs make it throttle, which "
+                     "holds a dense GEMM below the 2.4 GHz peak as well")}
 
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
