@@ -131,3 +131,27 @@ def test_without_lse_output():
                 torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert np.array_equal(o.float().cpu().numpy(), o_ref)
+
+
+# Each off-diagonal block's P is computed with the running max and accepted while its row sum
+# stays <= 2^12: tiles 0-2 are checked at the end of the pass that computed them, tile 3 just
+# before its P·V. Scores of some keys of key block 0 far above the rest (x6: P would overflow
+# fp16 without the exact-max path, leaving NaN in O) pick which check fails and where:
+#   keys 96-127 (tile 3 only) with rows [0, qb-1, qb]: the tile-3 check inside the loop
+#   keys 96-127 with rows [0, qb]: the tile-3 check in the last pass
+#   keys 0-95 with rows [0, qb]: the tiles-0-2 check of the last loop iteration
+#   keys 0-127 with rows [0, qb-2, qb-1, qb]: the tiles-0-2 check with blocks still ahead
+@pytest.mark.parametrize("keys,window", [((96, 128), 2), ((96, 128), 1), ((0, 96), 1),
+                                         ((0, 128), 3)])
+def test_speculation_fallbacks(keys, window):
+    B, H, T = 1, 2, 1024
+    rp, ci = P.global_csr(B, H, T, 1, window)
+    q, k, v = P.make_qkv(B, H, T, seed=70 + window)
+    k = k.clone()
+    k[:, :, keys[0]:keys[1]] *= 6.0
+    print(f"case fallback keys {keys} window {window}", flush=True)
+    o, lse = gp.run_csr_walk(q, k, v, rp, ci)
+    assert np.isfinite(o).all()
+    oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
+    assert_close(o, oo)
+    assert_close(lse, ol, what="LSE")
