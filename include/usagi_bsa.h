@@ -26,10 +26,10 @@
  *     and its return value), or NULL / 0 for the kernel's built-in order. Any plan of the same
  *     CSR gives bit-identical results: it only decides which GPU slot runs which query block.
  *   - stream: a hipStream_t (NULL = the default stream). The launch is asynchronous.
- *   - Kernel: fp16 calls without seq_lens whose rows hold at most 4 key blocks on average
+ *   - Kernel: calls without seq_lens whose rows hold at most 4 key blocks on average
  *     (max_nnz <= 4 * T/128, or the analytic pattern's own count) run a software-pipelined
  *     kernel; other calls, and every call when USAGI_BSA_PIPE=0 is set in the environment, run
- *     the two-phase kernel (USAGI_BSA_PIPE=1 makes every fp16 call without seq_lens on CSR or
+ *     the two-phase kernel (USAGI_BSA_PIPE=1 makes every call without seq_lens on CSR or
  *     analytic rows use the pipelined one; read at each launch). Both meet the same parity
  *     bound; between them results can differ in the last bits.
  *   - Return: 0 on success; a negative USAGI_BSA_E* code for a rejected argument; a positive

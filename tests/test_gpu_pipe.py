@@ -1,12 +1,11 @@
 """The pipelined kernel (bsa_fwd_pipe_kernel) on the GPU parity cases it can run.
 
-The library picks it by itself for short rows only (fp16, no seq_lens, CSR or analytic rows
-averaging at most 4 key blocks); USAGI_BSA_PIPE=1 makes it take every fp16 call without
-seq_lens, so the parity tests of the default walk and of the window path run again on it here
-(cases with seq_lens or bf16 inputs still run on bsa_fwd_dma_kernel). Left out are the tests whose
-point is bitwise equality with the other kernel (the generic walk, the seq_lens variant): the
-two kernels round differently within the parity tolerance (the row sum of P in fp32 here, from
-fp16 pairs there).
+The library picks it by itself for short rows only (no seq_lens, CSR or analytic rows averaging
+at most 4 key blocks); USAGI_BSA_PIPE=1 makes it take every such call, so the parity tests of
+the default walk and of the window path run again on it here, in fp16 and bf16 (cases with
+seq_lens still run on bsa_fwd_dma_kernel). Left out are the tests whose point is bitwise equality
+with the other kernel (the generic walk, the seq_lens variant): the two kernels round
+differently within the parity tolerance (the row sum of P in fp32 here, from fp16 pairs there).
 """
 
 from __future__ import annotations
@@ -35,6 +34,10 @@ test_plumbing_vs_dense_oracle = gp.test_plumbing_vs_dense_oracle
 test_full_size_every_head_vs_fp32_walk = gp.test_full_size_every_head_vs_fp32_walk
 test_full_size_rows_in_any_order_before_the_diagonal = gp.test_full_size_rows_in_any_order_before_the_diagonal
 test_random_csr = gp.test_random_csr
+test_bf16_inputs = gp.test_bf16_inputs
+test_bf16_full_size_every_head_vs_fp32_walk = gp.test_bf16_full_size_every_head_vs_fp32_walk
+test_bf16_running_max_growth = gp.test_bf16_running_max_growth
+test_window_path_bf16 = gp.test_window_path_bf16
 test_golden_fixtures = gp.test_golden_fixtures
 test_full_size_deterministic = gp.test_full_size_deterministic
 test_full_size_linear_in_v = gp.test_full_size_linear_in_v
@@ -67,21 +70,27 @@ def _csr_walk_with(mode, monkeypatch, q, k, v, rp, ci):
     return gp.run_csr_walk(q, k, v, rp, ci)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("w", [1, 2, 4])
-def test_short_rows_choose_the_pipelined_kernel(monkeypatch, w):
+def test_short_rows_choose_the_pipelined_kernel(monkeypatch, w, dtype):
     """Sliding windows of up to 4 blocks: the automatic choice gives bitwise the pipelined
     kernel's result, and both kernels agree with the dense oracle."""
     B, H, T = 1, 4, 2048
     rp, ci = P.sliding_csr(B, H, T, w)
     q, k, v = P.make_qkv(B, H, T, seed=30 + w)
-    print(f"case short rows sliding w{w}", flush=True)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    rtol = gp.BF16_RTOL if dtype == torch.bfloat16 else None
+    print(f"case short rows sliding w{w} {dtype}", flush=True)
     o_auto, l_auto = _csr_walk_with(None, monkeypatch, q, k, v, rp, ci)
     o_pipe, l_pipe = _csr_walk_with("1", monkeypatch, q, k, v, rp, ci)
     o_dma, l_dma = _csr_walk_with("0", monkeypatch, q, k, v, rp, ci)
     assert np.array_equal(o_auto, o_pipe) and np.array_equal(l_auto, l_pipe)
     oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
     for o, lse in ((o_pipe, l_pipe), (o_dma, l_dma)):
-        assert_close(o, oo)
+        if rtol is None:
+            assert_close(o, oo)
+        else:
+            assert_close(o, oo, rtol=rtol)
         assert_close(lse, ol, what="LSE")
 
 

@@ -726,7 +726,7 @@ void bsa_fwd_dma_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pipelined kernel (fp16, no seq_lens, CSR or analytic rows): the same work items, LDS layout and
+// Pipelined kernel (no seq_lens, CSR or analytic rows): the same work items, LDS layout and
 // per-wave rows as bsa_fwd_dma_kernel, but with Q·K^T of key block b_{i+1}, P·V of b_i and one key
 // tile's softmax interleaved instruction by instruction, K and V streamed through LDS in 8 KiB
 // sub-tiles. The work item after its coordinates is one generated asm statement
@@ -768,7 +768,7 @@ static_assert(USAGI_PIPE_LAST_VGPR == 175 && USAGI_PIPE_AGPRS == 64 && USAGI_PIP
 
 // No amdgpu_waves_per_eu here: with it the compiler refuses the asm statement's register
 // operands; 176 + 10 VGPRs and 64 AGPRs still give two waves per SIMD (checked by a test).
-template <int kRows>
+template <int kRows, bool kBf16>
 __global__ __launch_bounds__(kThreads)
 void bsa_fwd_pipe_kernel(Args a) {
   static_assert(kRows == kRowsCsr || kRows == kRowsWindow, "CSR or analytic rows only");
@@ -867,10 +867,14 @@ void bsa_fwd_pipe_kernel(Args a) {
     [haslse] "s"(has_lse), [krow] "v"(krow), [kx] "v"(kx), [vrow] "v"(vrow), [tq] "v"(tq64),       \
     [ko0] "v"(ko0), [ko1] "v"(ko1), [vo] "v"(vo), [qo] "v"(qo), [lid] "v"(lane)                   \
   : "memory", "vcc", "scc", "m0", USAGI_PIPE_CLOBBER_S, USAGI_PIPE_CLOBBER_V, USAGI_PIPE_CLOBBER_A
-  if constexpr (kRows == kRowsWindow) {
-    asm volatile(USAGI_PIPE_ASM_WINDOW USAGI_PIPE_OPERANDS);
+  if constexpr (kRows == kRowsWindow && kBf16) {
+    asm volatile(USAGI_PIPE_ASM_WINDOW_BF16 USAGI_PIPE_OPERANDS);
+  } else if constexpr (kRows == kRowsWindow) {
+    asm volatile(USAGI_PIPE_ASM_WINDOW_F16 USAGI_PIPE_OPERANDS);
+  } else if constexpr (kBf16) {
+    asm volatile(USAGI_PIPE_ASM_CSR_BF16 USAGI_PIPE_OPERANDS);
   } else {
-    asm volatile(USAGI_PIPE_ASM_CSR USAGI_PIPE_OPERANDS);
+    asm volatile(USAGI_PIPE_ASM_CSR_F16 USAGI_PIPE_OPERANDS);
   }
 #undef USAGI_PIPE_OPERANDS
 }
@@ -954,7 +958,7 @@ LaunchEvents take_events() {
   return e;
 }
 
-// Which kernel runs an fp16 call without seq_lens on CSR or analytic rows: bsa_fwd_pipe_kernel
+// Which kernel runs a call without seq_lens on CSR or analytic rows: bsa_fwd_pipe_kernel
 // when the rows hold at most kPipeMaxBlocks key blocks on average (the diagonal included), else
 // bsa_fwd_dma_kernel. A CSR's column list holds max_nnz entries per (b, h), so its rows average
 // at most max_nnz / nqb blocks; analytic rows count their entries exactly, which gives the
@@ -988,8 +992,8 @@ int launch(const Args& a, int slots, hipStream_t s, LaunchEvents ev) {
   const void* fn = a.seq_lens
                        ? reinterpret_cast<const void*>(&bsa_fwd_dma_kernel<kBf16, kRows, false>)
                        : reinterpret_cast<const void*>(&bsa_fwd_dma_kernel<kBf16, kRows, true>);
-  if constexpr (!kBf16 && (kRows == kRowsCsr || kRows == kRowsWindow)) {
-    if (!a.seq_lens && use_pipe(a, kRows)) fn = reinterpret_cast<const void*>(&bsa_fwd_pipe_kernel<kRows>);
+  if constexpr (kRows == kRowsCsr || kRows == kRowsWindow) {
+    if (!a.seq_lens && use_pipe(a, kRows)) fn = reinterpret_cast<const void*>(&bsa_fwd_pipe_kernel<kRows, kBf16>);
   }
   Args arg = a;
   void* params[] = {&arg};

@@ -364,9 +364,12 @@ def rescale_to(em, tiles):
 
 
 class Kernel:
-    def __init__(self, mode):
+    def __init__(self, mode, bf16=False):
         assert mode in ("csr", "window")
         self.mode = mode
+        self.bf16 = bf16
+        # Q·K^T in the input type; P·V always in fp16 (bf16 V is turned into fp16 in LDS)
+        self.qk_op = "v_mfma_f32_32x32x16_bf16" if bf16 else "v_mfma_f32_32x32x16_f16"
         self.em = Em()
         self.ool = []  # out-of-line blocks (fallbacks), appended after the epilogue
 
@@ -396,6 +399,8 @@ class Kernel:
             em.vm = []
         for op in pre:
             em.emit(*op)
+        if self.bf16:
+            self.convert_v(t)
         em.barrier()
         # MFMAs of the slot: Q·K^T steps and P·V (k-steps 2t, 2t+1) alternating
         qks = [("qk", s) for s in range(8)] if qk else []
@@ -455,7 +460,7 @@ class Kernel:
                 b = KR + 4 * (ki % D)
                 c = "0" if s == 0 else vrange(S(t), 16)
                 rd = vr(b, 4) + vr(Q(s), 4) + ([] if s == 0 else vr(S(t), 16))
-                em.emit("mfma", f"v_mfma_f32_32x32x16_f16 {vrange(S(t), 16)}, v[{b}:{b + 3}], v[{Q(s)}:{Q(s) + 3}], {c}",
+                em.emit("mfma", f"{self.qk_op} {vrange(S(t), 16)}, v[{b}:{b + 3}], v[{Q(s)}:{Q(s) + 3}], {c}",
                         rd, vr(S(t), 16))
             else:
                 vi = vq.index(m)
@@ -472,6 +477,28 @@ class Kernel:
                 else:
                     self.k_refill_branch(t, arg)
         em.wait_lgkm0()
+
+    def convert_v(self, t):
+        """bf16 inputs: this wave's two 1 KiB pieces of V sub-tile t (the rows its DMA wrote) are
+        turned into fp16 in place after they land and before the barrier that opens slot t, so
+        P·V runs on fp16 V as the reference's does. Each dword of two bf16 widens exactly to two
+        fp32 (a shift and a mask) and is packed to fp16 by one v_cvt_pk_f16_f32."""
+        em = self.em
+        a, lo, hi = T2 + 5, T2 + 3, T2 + 4
+        em.emit("valu", f"v_lshlrev_b32 v{a}, 4, {inp('lid')}", [], vr(a))
+        em.emit("valu", f"v_add_u32 v{a}, s{VL}, v{a}", vr(a) + sr(VL), vr(a))
+        for i in range(2):
+            em.emit("ds", f"ds_read_b128 v[{TMP + 4 * i}:{TMP + 4 * i + 3}], v{a} offset:{t * 8192 + 1024 * i}",
+                    vr(a), vr(TMP + 4 * i, 4))
+        for j in range(8):
+            d = TMP + j
+            em.emit("valu", f"v_lshlrev_b32 v{lo}, 16, v{d}", vr(d), vr(lo))
+            em.emit("valu", f"v_and_b32 v{hi}, 0xffff0000, v{d}", vr(d), vr(hi))
+            em.emit("valu", f"v_cvt_pk_f16_f32 v{d}, v{lo}, v{hi}", vr(lo) + vr(hi), vr(d))
+        for i in range(2):
+            em.emit("dsw", f"ds_write_b128 v{a}, v[{TMP + 4 * i}:{TMP + 4 * i + 3}] offset:{t * 8192 + 1024 * i}",
+                    vr(a) + vr(TMP + 4 * i, 4), [])
+        em.raw("s_waitcnt lgkmcnt(0)")
 
     def k_refill_branch(self, t, sub):
         """K(b_{i+2}, sub) refill when b_{i+2} exists, placeholder loads otherwise."""
@@ -572,7 +599,7 @@ class Kernel:
             b = ring[i]
             c = "0" if s == 0 else vrange(S(t), 16)
             rdregs = vr(b, 4) + vr(Q(s), 4) + ([] if s == 0 else vr(S(t), 16))
-            em.emit("mfma", f"v_mfma_f32_32x32x16_f16 {vrange(S(t), 16)}, v[{b}:{b + 3}], v[{Q(s)}:{Q(s) + 3}], {c}",
+            em.emit("mfma", f"{self.qk_op} {vrange(S(t), 16)}, v[{b}:{b + 3}], v[{Q(s)}:{Q(s) + 3}], {c}",
                     rdregs, vr(S(t), 16))
             if i + D < len(ops):
                 rd(i + D)
@@ -757,8 +784,9 @@ class Kernel:
                     em.emit("valu", f"v_accvgpr_read_b32 v{ov[k]}, a{16 * u + 4 * g + k}", ar(16 * u + 4 * g + k), vr(ov[k]))
                 for k in range(4):
                     em.emit("valu", f"v_mul_f32 v{ov[k]}, v{ov[k]}, v{inv}", vr(ov[k]) + vr(inv), vr(ov[k]))
-                em.emit("valu", f"v_cvt_pk_f16_f32 v{pk[0]}, v{ov[0]}, v{ov[1]}", vr(ov[0]) + vr(ov[1]), vr(pk[0]))
-                em.emit("valu", f"v_cvt_pk_f16_f32 v{pk[1]}, v{ov[2]}, v{ov[3]}", vr(ov[2]) + vr(ov[3]), vr(pk[1]))
+                cvt = "v_cvt_pk_bf16_f32" if self.bf16 else "v_cvt_pk_f16_f32"
+                em.emit("valu", f"{cvt} v{pk[0]}, v{ov[0]}, v{ov[1]}", vr(ov[0]) + vr(ov[1]), vr(pk[0]))
+                em.emit("valu", f"{cvt} v{pk[1]}, v{ov[2]}, v{ov[3]}", vr(ov[2]) + vr(ov[3]), vr(pk[1]))
                 c = 4 * u + g
                 em.emit("valu", f"v_xor_b32 v{addr}, {16 * c}, v{x16}", vr(x16), vr(addr))
                 em.emit("valu", f"v_add_u32 v{addr}, v{addr}, v{wb}", vr(addr) + vr(wb), vr(addr))
@@ -822,7 +850,7 @@ class Kernel:
 # ------------------------------------------------------------------------------------------
 
 HEADER = """// Generated by gen_bsa_pipe.py; do not edit. Inline assembly of bsa_fwd_pipe_kernel's work
-// item (one string per row kind). Operands: see the asm statement in bsa_fwd.hip.
+// item (one string per row kind and input type). Operands: see the asm statement in bsa_fwd.hip.
 """
 
 
@@ -836,8 +864,9 @@ def c_string(lines):
 
 def generate():
     parts = [HEADER]
-    for mode, name in (("csr", "USAGI_PIPE_ASM_CSR"), ("window", "USAGI_PIPE_ASM_WINDOW")):
-        k = Kernel(mode)
+    for mode, bf16, name in (("csr", False, "USAGI_PIPE_ASM_CSR_F16"), ("window", False, "USAGI_PIPE_ASM_WINDOW_F16"),
+                             ("csr", True, "USAGI_PIPE_ASM_CSR_BF16"), ("window", True, "USAGI_PIPE_ASM_WINDOW_BF16")):
+        k = Kernel(mode, bf16)
         lines = k.build()
         parts.append(f"#define {name} \\\n" + c_string(lines).replace("\n", " \\\n") + "\n")
     parts.append(f"#define USAGI_PIPE_SGPR_LO {SGPR_LO}\n#define USAGI_PIPE_SGPR_HI {SGPR_HI}\n"
