@@ -48,8 +48,21 @@ def hipcc_command(srcs: list[str] | None = None, out: str = LIB_PATH,
     ]
 
 
+def generate_asm() -> str:
+    """Write csrc/bsa_pipe_asm.inc (the pipelined kernel's work item as inline assembly) from its
+    generator, csrc/gen_bsa_pipe.py; returns its path."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("gen_bsa_pipe", os.path.join(CSRC_DIR, "gen_bsa_pipe.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    return gen.write()
+
+
 def build(verbose: bool = False) -> str:
-    """Compile the HIP source into an in-tree shared library; returns its path."""
+    """Generate the pipelined kernel's assembly, then compile the HIP source into an in-tree
+    shared library; returns its path."""
+    generate_asm()
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
     cmd = hipcc_command(out=tmp)

@@ -30,7 +30,8 @@ a VALU: 1; a VALU result by v_permlane32_swap: 2; an SGPR written by SALU read b
 instruction: 1, by VALU: 5) and inserts s_nop where the instruction stream does not already
 space them; LDS and global load results are waited for with counted s_waitcnt.
 
-Run:  python3 usagi_amd/csrc/gen_bsa_pipe.py   (writes bsa_pipe_asm.inc next to this file)
+usagi_amd/build.py runs it before every compile (python3 usagi_amd/csrc/gen_bsa_pipe.py writes
+bsa_pipe_asm.inc next to this file; --check compares an existing file with its output).
 """
 from __future__ import annotations
 
@@ -86,7 +87,6 @@ SKB = 77  # key block of a lookup
 SREAL = 78  # 1 when b_{i+2} exists
 ST2 = 79
 SCB = 80  # s[80:81] column list base (CSR)
-ST3 = 82
 KHB = 84  # s[84:85] K of this (b, h)
 VHB = 86  # s[86:87] V of this (b, h)
 KL = 88  # LDS: K buffer + 2048 * wave (this wave's DMA rows of a sub-tile)
@@ -874,8 +874,23 @@ def generate():
     return "\n".join(parts)
 
 
+OUT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "bsa_pipe_asm.inc")
+
+
+def write(path: str = OUT_PATH) -> str:
+    """Write the include file (only if its contents change) and return its path."""
+    text = generate()
+    cur = open(path).read() if os.path.exists(path) else None
+    if cur != text:
+        tmp = path + ".tmp"
+        with open(tmp, "w") as f:
+            f.write(text)
+        os.replace(tmp, path)
+    return path
+
+
 def main(argv):
-    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "bsa_pipe_asm.inc")
+    out = OUT_PATH
     text = generate()
     if len(argv) > 1 and argv[1] == "--check":
         cur = open(out).read() if os.path.exists(out) else ""
