@@ -338,7 +338,7 @@ def row_max(em, tiles, dst):
 
 def rescale_to(em, tiles):
     """Move the row max to max(m, exact max of the given S tiles * scale); rescale l and O."""
-    mx, alpha, tmp = T2 + 2, T2 + 3, T2 + 4
+    mx, alpha = T2 + 2, T2 + 3
     row_max(em, tiles, mx)
     pair_reduce(em, mx, "v_max_f32")
     em.emit("valu", f"v_mul_f32 v{mx}, {inp('scale')}, v{mx}", vr(mx), vr(mx))
@@ -626,7 +626,6 @@ class Kernel:
         skip = self.L(f"nok1_{w}")
         em.raw(f"s_cmp_eq_u32 {inp('noff')}, 0")
         em.raw(f"s_cbranch_scc1 {skip}")
-        snap_vm = list(em.vm)
         for sub in range(3):
             emit_ops(em, dma_ops(KBB, sub, KL, ("ko0", "ko1")))
         em.out.append(f"{skip}:")
@@ -668,10 +667,10 @@ class Kernel:
             em.raw(f"v_min_u32 v{T2}, s{ST}, v{T2}")
             em.raw(f"v_lshlrev_b32 v{T2}, 2, v{T2}")
             em.raw(f"s_mov_b64 s[{SCB}:{SCB + 1}], {inp('c')}")
-            em.raw("s_nop 4")
+            em.raw("s_nop 4")  # the SALU-written base and VALU-written offset before the load
             em.raw(f"global_load_dword {inp('colv')}, v{T2}, s[{SCB}:{SCB + 1}]")
-            em.raw("s_waitcnt vmcnt(0)")
-            em.raw("s_nop 4")
+            em.raw("s_waitcnt vmcnt(0)")  # also drains the tile DMAs: once per 64 entries
+            em.raw("s_nop 4")  # colv before the v_readlane of the next lookup
             em.out.append(f"{norl}:")
             em.last_w = {}
             em.nops(5)
