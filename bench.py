@@ -354,6 +354,37 @@ def trace_summary(trace_csv: str, bench_json: str) -> int:
 FAM_ORDER = P.FAMILIES
 
 
+def sclk_under_load(fn, seconds: float = 0.8):
+    """Median of the shader clock rocm-smi reports (MHz) while fn runs back to back, or None
+    when rocm-smi is not there."""
+    import threading
+
+    samples = []
+
+    def sample():
+        time.sleep(seconds / 3)
+        for _ in range(2):
+            try:
+                r = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True,
+                                   timeout=10)
+                m = re.search(r"sclk[^\n]*\((\d+)\s*Mhz\)", r.stdout, re.I)
+                if m:
+                    samples.append(int(m.group(1)))
+            except (OSError, subprocess.SubprocessError):
+                pass
+            time.sleep(seconds / 4)
+
+    th = threading.Thread(target=sample)
+    th.start()
+    t0 = time.perf_counter()
+    while th.is_alive() or time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+    th.join()
+    return int(np.median(samples)) if samples else None
+
+
 def event_pair():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -718,6 +749,8 @@ def main() -> int:
         zfn = [lambda: block_sparse_attn_fwd(qz, kz, vz, *dev_csr["sliding"], None)]
         warm(zfn, args.min_warmup_s)
         zero_ms = float(np.median(time_calls(zfn, args.steps, stream)[0]))
+        clk_zero = sclk_under_load(zfn[0])
+        clk_random = sclk_under_load(lambda: call("sliding"))
         del qz, kz, vz
         gfn = [lambda: torch.matmul(ga, gb, out=gc)]
         warm(gfn, args.min_warmup_s)
@@ -728,11 +761,14 @@ def main() -> int:
             "sliding_zero_inputs_ms": round(zero_ms, 4),
             "sliding_random_inputs_ms": round(fam_out["sliding"]["median_ms"], 4),
             "ratio_random_to_zero": round(fam_out["sliding"]["median_ms"] / zero_ms, 4),
+            "sclk_mhz_sliding_random_inputs": clk_random,
+            "sclk_mhz_sliding_zero_inputs": clk_zero,
             "dense_fp16_gemm_tflops": round(gemm_tflops, 1),
             "dense_fp16_gemm_frac_peak": round(gemm_tflops / PEAK_FP16_TFLOPS, 4),
             "note": ("call medians on the same box after the timed steps; all-zero inputs keep "
                      "the part at its top clock, random fp16 inputs make it throttle, which "
-                     "holds a dense GEMM below the 2.4 GHz peak as well")}
+                     "holds a dense GEMM below the 2.4 GHz peak as well; sclk as rocm-smi "
+                     "reports it while the sliding family runs back to back")}
 
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
