@@ -60,6 +60,7 @@ from usagi_amd import patterns as P  # noqa: E402
 
 METRIC = "geomean fwd ms @B2 H16 T8192 D128 over 3 sparsity families; % fp16 MFMA peak"
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, published
+PEAK_SCLK_MHZ = 2400  # the shader clock the published peak is quoted at
 FLOP_PER_BLOCK = 4 * 128 ** 3
 # MFMAs the kernel issues for a diagonal block: 160 of a full block's 256 (each wave skips the
 # key tiles above its 32 query rows in Q·K^T and the k-steps above them in P·V).
@@ -756,6 +757,7 @@ def main() -> int:
         warm(gfn, args.min_warmup_s)
         gemm_ms = float(np.median(time_calls(gfn, args.steps, stream)[0]))
         gemm_tflops = 2.0 * 8192 ** 3 / gemm_ms / 1e9
+        clk_gemm = sclk_under_load(gfn[0])
         del ga, gb, gc
         extra_cfg["power_context"] = {
             "sliding_zero_inputs_ms": round(zero_ms, 4),
@@ -763,12 +765,16 @@ def main() -> int:
             "ratio_random_to_zero": round(fam_out["sliding"]["median_ms"] / zero_ms, 4),
             "sclk_mhz_sliding_random_inputs": clk_random,
             "sclk_mhz_sliding_zero_inputs": clk_zero,
+            # the fraction of the MFMA peak at the clock the part held (peak quoted at 2.4 GHz)
+            "sliding_frac_peak_at_sclk": (round(fam_out["sliding"]["frac_peak"] * PEAK_SCLK_MHZ
+                                                / clk_random, 4) if clk_random else None),
             "dense_fp16_gemm_tflops": round(gemm_tflops, 1),
             "dense_fp16_gemm_frac_peak": round(gemm_tflops / PEAK_FP16_TFLOPS, 4),
+            "sclk_mhz_dense_fp16_gemm": clk_gemm,
             "note": ("call medians on the same box after the timed steps; all-zero inputs keep "
                      "the part at its top clock, random fp16 inputs make it throttle, which "
                      "holds a dense GEMM below the 2.4 GHz peak as well; sclk as rocm-smi "
-                     "reports it while the sliding family runs back to back")}
+                     "reports it while the sliding family, or the GEMM, runs back to back")}
 
     achieved = (sum(flops) / len(flops)) / mean_launch / 1e9  # TFLOP/s: mean FLOP / mean duration
     traffic = read_traffic()
