@@ -150,17 +150,22 @@ def test_without_lse_output():
 #   keys 96-127 with rows [0, qb]: the tile-3 check in the last pass
 #   keys 0-95 with rows [0, qb]: the tiles-0-2 check of the last loop iteration
 #   keys 0-127 with rows [0, qb-2, qb-1, qb]: the tiles-0-2 check with blocks still ahead
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("keys,window", [((96, 128), 2), ((96, 128), 1), ((0, 96), 1),
                                          ((0, 128), 3)])
-def test_speculation_fallbacks(keys, window):
+def test_speculation_fallbacks(keys, window, dtype):
     B, H, T = 1, 2, 1024
     rp, ci = P.global_csr(B, H, T, 1, window)
     q, k, v = P.make_qkv(B, H, T, seed=70 + window)
     k = k.clone()
     k[:, :, keys[0]:keys[1]] *= 6.0
-    print(f"case fallback keys {keys} window {window}", flush=True)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    print(f"case fallback keys {keys} window {window} {dtype}", flush=True)
     o, lse = gp.run_csr_walk(q, k, v, rp, ci)
     assert np.isfinite(o).all()
     oo, ol = bsa_oracle.dense_masked(q, k, v, rp, ci)
-    assert_close(o, oo)
+    if dtype == torch.bfloat16:
+        assert_close(o, oo, rtol=gp.BF16_RTOL)
+    else:
+        assert_close(o, oo)
     assert_close(lse, ol, what="LSE")
