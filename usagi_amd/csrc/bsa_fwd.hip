@@ -19,14 +19,17 @@
 //
 // MI355X design points (not a translation of the Triton program):
 //   * One 256-thread workgroup (4 wave64s) per (b*h, qb), or per slot of a host work plan; each
-//     wave owns 32 query rows; two workgroups per CU (64 KiB LDS, <= 240 VGPRs each).
-//   * Everything is computed transposed so that one lane owns one query row:
+//     wave owns 32 query rows; two workgroups per CU (64 KiB LDS, <= 256 VGPRs each).
+//   * Everything is computed transposed, so that a lane's values all belong to its query rows:
 //       S^T[key][q] = K · Q^T      (MFMA A = K rows from LDS, B = Q fragment in VGPRs)
 //       O^T[d][q]  += V^T · P^T    (MFMA A = V^T read with ds_read_b64_tr_b16 from the row-major
 //                                   V tile, B = P taken straight from the S^T accumulators)
-//     With v_mfma_f32_32x32x16_{f16,bf16}, lane l holds query (l % 32); the other 64 keys of
-//     that query sit in lane l ^ 32, so the row max is one v_permlane32_swap and the running
-//     row sum needs no cross-lane work until the epilogue.
+//     With v_mfma_f32_16x16x32_{f16,bf16} a wave's 32 query rows are two 16-row tiles: lane l
+//     holds query (l % 16) of each and keys 4(l / 16) .. +3 of every 16-key tile, so the keys of
+//     a query sit in lanes l, l^16, l^32, l^48; the row max is two swaps (v_permlane16_swap,
+//     v_permlane32_swap) and the running row sum needs no cross-lane work until the epilogue.
+//     On random data the part is held by its power limit, and this shape, which moves half the
+//     accumulator bytes per FLOP of 32x32x16, runs the same instruction mix at a higher clock.
 //   * K/V tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), XOR-swizzled,
 //     and their DMA pieces are interleaved with the other product's MFMAs.
 //   * Work order without a plan (item_coords): query blocks from the last one down; when B*H is
@@ -63,7 +66,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -121,6 +124,20 @@ __device__ __forceinline__ float wave_pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Max / sum over lanes l, l^16, l^32, l^48 (the four lane groups that hold one query row in the
+// 16x16 MFMA layouts): {x[l], x[l ^ 16]} then {y[l], y[l ^ 32]}, each in some order.
+__device__ __forceinline__ float wave_quad_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return wave_pair_max(y);
+}
+
+__device__ __forceinline__ float wave_quad_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  return wave_pair_sum(y);
+}
+
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -144,12 +161,12 @@ __device__ __forceinline__ uint32_t pack_out(float x, float y) {
 }
 
 template <bool kBf16>
-__device__ __forceinline__ floatx16 mfma_qk(u32x4 a, u32x4 b, floatx16 c) {
+__device__ __forceinline__ floatx4 mfma_qk16(u32x4 a, u32x4 b, floatx4 c) {
   if constexpr (kBf16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
                                                   __builtin_bit_cast(half8, b), c, 0, 0, 0);
   }
 }
@@ -162,8 +179,10 @@ __device__ __forceinline__ floatx16 mfma_qk(u32x4 a, u32x4 b, floatx16 c) {
 // keeps the matrix core busy.
 //
 // LDS tiles are 128 rows x 256 B, unpadded, with 16-byte chunks XOR-swizzled inside each row
-// (K: chunk ^ (row % 16), V: chunk ^ 4 * (row % 4)) so that both the DMA writes (1 KiB
-// lane-contiguous per wave instruction) and the MFMA operand reads spread over all banks.
+// (K: chunk ^ (row % 16), V: chunk ^ 2 * (row % 8)) so that the DMA writes (1 KiB
+// lane-contiguous per wave instruction) fill whole rows and the MFMA operand reads spread over
+// all 64 banks: a ds_read_b128 serves 16 lanes per cycle (16 rows of K, one chunk each), a
+// ds_read_b64_tr_b16 32 lanes (8 consecutive rows of V, the same two chunks of each).
 //
 // Per key block j (two barriers, tiles single-buffered per workgroup, 64 KiB of LDS):
 //   wait K(j) | barrier | S^T = K·Q^T, DMA of V(j) spread between the MFMAs | P = exp2 in fp16
@@ -248,8 +267,10 @@ void bsa_fwd_dma_kernel(Args a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 31;
-  const int lh = lane >> 5;
+  // v_mfma_f32_16x16x32 layouts: lane L holds column c16 = L % 16 of a 16x16 product tile and
+  // rows 4*g4 .. 4*g4+3 (g4 = L / 16); an operand holds row c16 and k = 8*g4 .. 8*g4+7.
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
 
   int qb, bh;
   if (a.sched) {
@@ -271,13 +292,13 @@ void bsa_fwd_dma_kernel(Args a) {
   // per-lane byte offsets repeat for every tile, so only the uniform tile base changes.
   const int dma_r = lane >> 4;
   const int dma_pc = lane & 15;
-  // Row 32w + 4i + L/16 has (row % 16) = 4(i % 4) + L/16 and (row % 4) = L/16.
+  // Row 32w + 4i + L/16 has (row % 16) = 4(i % 4) + L/16 and (row % 8) = 4(i % 2) + L/16.
   uint32_t k_off[4];
   uint32_t v_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     k_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * i + dma_r)));
-    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (4 * dma_r)));
+    v_off[i] = (uint32_t)((32 * wave + dma_r) * 256 + 16 * (dma_pc ^ (8 * (i & 1) + 2 * dma_r)));
   }
   const uint32_t k_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(k_lds) + wave * 8192);
   const uint32_t v_dst = __builtin_amdgcn_readfirstlane(lds_addr_of(v_lds) + wave * 8192);
@@ -305,15 +326,24 @@ void bsa_fwd_dma_kernel(Args a) {
     }
   }
 
-  const int q_local = wave * 32 + li;
-  const int qrow = q0 + q_local;
-  const bool qvalid = kFullSeq || qrow < seq_len;
-
-  u32x4 qf[8];
-  {
-    const uint16_t* qp = a.q + base + (size_t)qrow * kHd + 8 * lh;
+  // The wave's 32 query rows are two 16-row tiles qt = 0, 1; lane L holds row c16 of each.
+  int q_local[2];
+  int qrow[2];
+  bool qvalid[2];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = *(const u32x4*)(qp + 16 * s);
+  for (int qt = 0; qt < 2; ++qt) {
+    q_local[qt] = wave * 32 + 16 * qt + c16;
+    qrow[qt] = q0 + q_local[qt];
+    qvalid[qt] = kFullSeq || qrow[qt] < seq_len;
+  }
+
+  // Q^T operands (MFMA B, 32 d x 16 queries): tile qt, k-step ks holds d = 32ks + 8g4 .. +7.
+  u32x4 qf[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const uint16_t* qp = a.q + base + (size_t)qrow[qt] * kHd + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[qt][ks] = *(const u32x4*)(qp + 32 * ks);
   }
 
   const int nqb_m1 = a.nqb - 1;
@@ -410,23 +440,28 @@ void bsa_fwd_dma_kernel(Args a) {
     }
   };
 
-  // K operand (MFMA A, 32 keys x 16 d): lane reads row 32t + li, logical chunk 2s + lh.
-  const char* k_rd = (const char*)k_lds + li * 256;
-  const int k_x = lh ^ (li & 15);
-  // V^T operand via transpose reads: source lane l supplies row key0 + (l%16)/4 and the
-  // 8 bytes at d = 32u + 16((l/16)%2) + 4(l%4); key0 = 16s + 8r + 4lh.
-  const int tq = (lane & 15) >> 2;
-  const int t_x = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-  const char* v_rd = (const char*)v_lds + (4 * lh + tq) * 256 + 8 * (lane & 1);
+  // K operand (MFMA A, 16 keys x 32 d) of key tile t (keys 16t .. 16t+15), k-step ks: lane reads
+  // row 16t + c16, logical chunk 4ks + g4, stored at chunk (4ks + g4) ^ c16 = 4ks ^ k_x.
+  const char* k_rd = (const char*)k_lds + c16 * 256;
+  const int k_x = g4 ^ c16;
+  // V^T operand (MFMA A, 16 d x 32 keys) of d-tile u, k-step ks, from two transpose reads: in
+  // lane group g4 source lane c16 supplies row key0 + c16/4 and the 8 bytes at d = 16u + 4(c16%4),
+  // with key0 = 32ks + 4g4 for k-slots 8g4 .. 8g4+3 and key0 + 16 for 8g4+4 .. 8g4+7. That is the
+  // key order in which the S^T tiles 2ks and 2ks+1 hand this lane its 8 values of P, so the
+  // MFMA's sum over k runs over the 32 keys of the step. Logical chunk 2u + (c16%4)/2 of a row
+  // with row % 8 = 4(g4 % 2) + c16/4 is stored at chunk (2u + (c16%4)/2) ^ 2(row % 8) = 2u ^ v_x.
+  const char* v_rd = (const char*)v_lds + (4 * g4 + (c16 >> 2)) * 256 + 8 * (c16 & 1);
+  const int v_x = 8 * (g4 & 1) + 2 * (c16 >> 2) + ((c16 & 3) >> 1);
 
-  floatx16 o_acc[4];
+  // O^T accumulators: query tile qt, d-tile u (d = 16u + 4g4 .. +3 of row c16).
+  floatx4 o_acc[2][8];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[u][r] = 0.0f;
+    for (int u = 0; u < 8; ++u) o_acc[qt][u] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  float m_used = -1e30f;
-  float l_part = 0.0f;
+  float m_used[2] = {-1e30f, -1e30f};
+  float l_part[2] = {0.0f, 0.0f};
   const float scale = a.qk_scale;
 
   // vmcnt(0): Q, the column chunk (CSR rows) and the first K tile have landed. Issued as a
@@ -450,59 +485,68 @@ void bsa_fwd_dma_kernel(Args a) {
     // workgroup) can issue, the MFMA stream goes first and the other wave's exponentials fill
     // the gaps.
     __builtin_amdgcn_s_setprio(1);
-    // ---- S^T = K · Q^T: 32 MFMAs, K operands read one step ahead.
-    floatx16 st[4];
+    // ---- S^T = K · Q^T: 64 MFMAs (16x16x32). Fragment f = 8ks + t (key tile t, k-step ks) is
+    // read four fragments ahead and feeds the MFMAs of both query tiles.
+    floatx4 st[2][8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st[t][r] = 0.0f;
+      for (int t = 0; t < 8; ++t) st[qt][t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    // V(j) DMA pieces go out between the QK MFMAs (the V buffer is free after the barrier).
+    // On the diagonal, key tile t (keys 16t .. 16t+15) lies above every row of query tile qt
+    // when t > 2w + qt (w = wave): those products are skipped, so are the fragments no query tile
+    // uses (t > 2w + 1), the softmax of the k-steps ks > w and their P·V.
+    auto k_needed = [&](int f) { return !kDiag || (f & 7) <= 2 * wave + 1; };
+    auto k_read = [&](int f) {
+      return *(const u32x4*)(k_rd + (f & 7) * 4096 + 16 * ((4 * (f >> 3)) ^ k_x));
+    };
     u32x4 kop[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (!kDiag || t <= wave) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * (0 ^ k_x));
+    for (int f = 0; f < 4; ++f) {
+      if (k_needed(f)) kop[f] = k_read(f);
     }
-    // On the diagonal, key tile t (keys 32t .. 32t+31) lies above every row of wave w when t > w:
-    // those tiles are skipped here, in the softmax and in P·V.
+    // V(j) DMA pieces go out between the MFMAs (the V buffer is free after the barrier).
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int f = 0; f < 32; ++f) {
+      const int t = f & 7;
+      const int ks = f >> 3;
+      const u32x4 ka = kop[f & 3];
+      if (f + 4 < 32 && k_needed(f + 4)) kop[f & 3] = k_read(f + 4);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (!kDiag || t <= wave) {
-          const u32x4 ka = kop[t];
-          if (s < 7) kop[t] = *(const u32x4*)(k_rd + t * 8192 + 16 * ((2 * (s + 1)) ^ k_x));
-          st[t] = mfma_qk<kBf16>(ka, qf[s], st[t]);
-        }
+      for (int qt = 0; qt < 2; ++qt) {
+        if (!kDiag || t <= 2 * wave + qt) st[qt][t] = mfma_qk16<kBf16>(ka, qf[qt][ks], st[qt][t]);
       }
-      dma_piece(vt_src, v_off, v_dst, s);
+      if ((f & 3) == 3) dma_piece(vt_src, v_off, v_dst, f >> 2);
     }
-    // Schedule: each step's 4 K operands are read one step ahead of its 4 MFMAs (deeper
-    // read-ahead only adds registers: the reads complete within one step).
+    // Schedule: the fragment four ahead is read before each pair of MFMAs.
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
 #pragma unroll
-    for (int i = 0; i < 7; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+    for (int i = 0; i < 28; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
 
-    // ---- masks (v7:94, v7:119-122), row max, speculative P
+    // ---- masks (v7:94, v7:119-122), row max, speculative P. S^T tile t of query tile qt holds
+    // keys 16t + 4g4 .. +3 of query row q_local[qt].
     if constexpr (kDiag) {
-      // Key tiles below the wave's own (t < wave) are visible to all its rows, its own tile
-      // (t == wave) takes the causal mask, and the tiles above (t > wave) were skipped by the
-      // MFMAs: their softmax is skipped too (P·V never reads them).
+      // Key tiles below query tile qt's own (t < 2w + qt) are visible to all its rows, its own
+      // (t == 2w + qt) takes the causal mask; tile 2w + 1 of query tile 0 lies above its rows
+      // but shares a k-step with tile 2w, so its P is made zero here.
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t == wave) {
+      for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = 32 * t + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (key > q_local || !qvalid) st[t][r] = -INFINITY;
+        for (int t = 0; t < 8; ++t) {
+          if (t > 2 * wave + qt) {
+            if (t <= 2 * wave + 1) st[qt][t] = floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          } else if (t == 2 * wave + qt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (4 * g4 + r > c16 || !qvalid[qt]) st[qt][t][r] = -INFINITY;
+            }
+          } else if (!qvalid[qt]) {
+            st[qt][t] = floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
           }
-        } else if (t < wave && !qvalid) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
         }
       }
     } else {
@@ -511,96 +555,105 @@ void bsa_fwd_dma_kernel(Args a) {
         // seq_len for an entry above it (every key of an earlier block is below this query
         // block, which starts below seq_len).
         if (kb >= qb) {
-          int last = kb == qb ? q_local : kBlk - 1;
-          if constexpr (!kFullSeq) {
-            if (kb > qb) last = min(last, seq_len - 1 - kb * kBlk);
-          }
-          const int lim = last - 4 * lh;
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
+          for (int qt = 0; qt < 2; ++qt) {
+            int last = kb == qb ? q_local[qt] : kBlk - 1;
+            if constexpr (!kFullSeq) {
+              if (kb > qb) last = min(last, seq_len - 1 - kb * kBlk);
+            }
+            const int lim = last - 4 * g4;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              if (32 * t + 8 * (r >> 2) + (r & 3) > lim) st[t][r] = -INFINITY;
+            for (int t = 0; t < 8; ++t) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                if (16 * t + r > lim) st[qt][t][r] = -INFINITY;
+              }
             }
           }
         }
       }
       if constexpr (kMaskQ) {
-        if (!qvalid) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
+        for (int qt = 0; qt < 2; ++qt) {
+          if (!qvalid[qt]) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) st[t][r] = -INFINITY;
+            for (int t = 0; t < 8; ++t) st[qt][t] = floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
           }
         }
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    // ---- P = exp2(S·scale - m) in fp16 and its row sum (this lane's 64 keys).
+    // ---- P = exp2(S·scale - m) in fp16 and its row sum (this lane's 32 keys of each row).
     // The diagonal block (always the first block of a row) takes the exact row max. Later blocks
     // compute P with the running max as it stands: each P is <= the lane's fp32 sum of its P,
     // so a sum <= 2^12 proves every P finite in fp16 and the result exact in the normalised
     // output; otherwise (rare) the row max moves to the block's exact max, O and l are rescaled
     // and P recomputed.
-    half8 pb[8];
-    float pblk = 0.0f;
+    // pb[qt][ks] is the P^T operand (MFMA B, 32 keys x 16 queries) of k-step ks: k-slots
+    // 8g4 .. 8g4+3 from S^T tile 2ks, 8g4+4 .. 8g4+7 from tile 2ks + 1.
+    half8 pb[2][4];
+    float pblk[2] = {0.0f, 0.0f};
     auto make_p = [&]() {
-      const float neg_m = -m_used;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (kDiag && (s >> 1) > wave) continue;  // a key tile above the wave's rows
+      for (int qt = 0; qt < 2; ++qt) {
+        const float neg_m = -m_used[qt];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pb[s][e] = (_Float16)__builtin_amdgcn_exp2f(fmaf(st[s >> 1][8 * (s & 1) + e], scale, neg_m));
+        for (int ks = 0; ks < 4; ++ks) {
+          if (kDiag && ks > wave) continue;  // keys above the wave's rows
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            pb[qt][ks][e] = (_Float16)__builtin_amdgcn_exp2f(
+                fmaf(st[qt][2 * ks + (e >> 2)][e & 3], scale, neg_m));
+          }
         }
-      }
-      float acc = 0.0f;
+        float acc = 0.0f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (kDiag && (s >> 1) > wave) continue;
+        for (int ks = 0; ks < 4; ++ks) {
+          if (kDiag && ks > wave) continue;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const half2 pp = {pb[s][2 * e], pb[s][2 * e + 1]};
-          acc = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, acc, false);
+          for (int e = 0; e < 4; ++e) {
+            const half2 pp = {pb[qt][ks][2 * e], pb[qt][ks][2 * e + 1]};
+            acc = __builtin_amdgcn_fdot2(pp, half2{1.0f16, 1.0f16}, acc, false);
+          }
         }
+        pblk[qt] = acc;
       }
-      pblk = acc;
     };
-    auto row_max = [&]() {
-      float mx = st[0][0];
+    auto row_max = [&](int qt) {
+      float mx = st[qt][0][0];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (kDiag && t > wave) continue;
+      for (int t = 0; t < 8; ++t) {
+        if (kDiag && t > 2 * wave + qt) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[t][r]);
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[qt][t][r]);
       }
-      return wave_pair_max(mx);
+      return wave_quad_max(mx);
     };
-    auto rescale = [&](float m_new) {
-      const float alpha = __builtin_amdgcn_exp2f(m_used - m_new);
-      m_used = m_new;
-      l_part *= alpha;
+    auto rescale = [&](int qt, float m_new) {
+      const float alpha = __builtin_amdgcn_exp2f(m_used[qt] - m_new);
+      m_used[qt] = m_new;
+      l_part[qt] *= alpha;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[u][r] *= alpha;
-      }
+      for (int u = 0; u < 8; ++u) o_acc[qt][u] *= alpha;
     };
     if constexpr (kDiag) {
       // The diagonal block is the item's first: O and l are still zero, so the row max is taken
       // without a rescale.
-      m_used = fmaxf(m_used, row_max() * scale);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) m_used[qt] = fmaxf(m_used[qt], row_max(qt) * scale);
       make_p();
     } else {
       make_p();
-      asm volatile("" ::"v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]), "v"(pb[4]), "v"(pb[5]),
-                   "v"(pb[6]), "v"(pb[7]));
-      if (__builtin_expect(__any(!(pblk <= kSpecSum)), 0)) {
-        rescale(fmaxf(m_used, row_max() * scale));
+      asm volatile("" ::"v"(pb[0][0]), "v"(pb[0][1]), "v"(pb[0][2]), "v"(pb[0][3]), "v"(pb[1][0]),
+                   "v"(pb[1][1]), "v"(pb[1][2]), "v"(pb[1][3]));
+      if (__builtin_expect(__any(!(pblk[0] <= kSpecSum) || !(pblk[1] <= kSpecSum)), 0)) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) rescale(qt, fmaxf(m_used[qt], row_max(qt) * scale));
         make_p();
       }
     }
-    l_part += pblk;
+    l_part[0] += pblk[0];
+    l_part[1] += pblk[1];
 
     USAGI_WAIT_VM(0);  // V(j) has landed
     if constexpr (kBf16) {
@@ -627,29 +680,48 @@ void bsa_fwd_dma_kernel(Args a) {
     const char* kt_src = kNext ? tile_k(key_block(j + 1)) : nullptr;
 
     __builtin_amdgcn_s_setprio(1);
-    // ---- O^T += V^T · P^T (32 MFMAs, V operands 2 ahead)
+    // ---- O^T += V^T · P^T (64 MFMAs, 16x16x32): each V^T fragment (d-tile u, k-step ks) feeds
+    // the MFMAs of both query tiles.
+    // Fragment g = 8ks + u (d-tile u, k-step ks), read four fragments ahead.
+    auto v_needed = [&](int g) { return !(kDiag && (g >> 3) > wave); };
+    auto v_read = [&](int g) {
+      const char* vb = v_rd + (g >> 3) * 8192 + 16 * ((2 * (g & 7)) ^ v_x);
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 4096));
+      return __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi),
+                                     0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    half8 vop[4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int g = 0; g < 4; ++g) {
+      if (v_needed(g)) vop[g] = v_read(g);
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        // Diagonal: k-step s holds keys 16s .. 16s+15, all above wave w's rows when s > 2w + 1.
-        if (kDiag && s > 2 * wave + 1) continue;
-        const char* vb = v_rd + 16 * (4 * (u ^ tq) + t_x) + s * 4096;
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vb);
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vb + 2048));
-        const half8 va = __builtin_shufflevector(__builtin_bit_cast(half4, lo),
-                                                 __builtin_bit_cast(half4, hi), 0, 1, 2, 3, 4, 5, 6, 7);
-        o_acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s], o_acc[u], 0, 0, 0);
+    for (int g = 0; g < 32; ++g) {
+      const int ks = g >> 3;
+      const int u = g & 7;
+      // Diagonal: k-step ks holds keys 32ks .. 32ks+31, all above wave w's rows when ks > w.
+      const half8 va = vop[g & 3];
+      if (g + 4 < 32 && v_needed(g + 4)) vop[g & 3] = v_read(g + 4);
+      if (v_needed(g)) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          o_acc[qt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt][ks], o_acc[qt][u], 0, 0, 0);
+        }
       }
       // K(j+1) DMA pieces between the P·V MFMAs (the K buffer is free after the barrier).
-      if constexpr (kNext) dma_piece(kt_src, k_off, k_dst, s);
+      if constexpr (kNext) {
+        if ((u & 3) == 3) dma_piece(kt_src, k_off, k_dst, 2 * ks + (u >> 2));
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    // Schedule: the fragment four ahead is read (two transpose reads) after each pair of MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 2);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    for (int i = 0; i < 28; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 2);
     __builtin_amdgcn_s_setprio(0);
     // No closing barrier: the next block's first barrier orders every wave's reads of this V
     // tile before the DMA of the next one, which is issued after it.
@@ -673,12 +745,17 @@ void bsa_fwd_dma_kernel(Args a) {
   for (int j = 0; j < n_off - 1; ++j) block(F_{}, MaskQ{}, T_{}, j);
   if (n_off > 0) block(F_{}, MaskQ{}, F_{}, n_off - 1);
 
-  const float l_tot = wave_pair_sum(l_part);
-  float inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;
-  if (!qvalid) inv = 0.0f;
+  float l_tot[2];
+  float inv[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    l_tot[qt] = wave_quad_sum(l_part[qt]);
+    inv[qt] = l_tot[qt] > 0.0f ? 1.0f / l_tot[qt] : 1.0f;
+    if (!qvalid[qt]) inv[qt] = 0.0f;
+  }
   // O: normalise, stage this wave's 32 rows in its 8 KiB slice of the K tile and store whole
   // 256-byte rows (1 KiB contiguous per instruction); written straight from the accumulator
-  // layout, each store instruction would touch 32 rows with 8 bytes each. The last block DMA'd
+  // layout, each store instruction would touch 16 rows with 8 bytes each. The last block DMA'd
   // no K tile and every wave finished reading its K at that block's second barrier, so the
   // K tile is free.
   {
@@ -686,26 +763,29 @@ void bsa_fwd_dma_kernel(Args a) {
     // Rows past seq_len were computed on whatever their Q holds: their O is cleared by a select
     // (never a multiply), and inv is 0 for them.
     if constexpr (!kFullSeq) {
-      if (!__all(qvalid)) {
+      if (!__all(qvalid[0] && qvalid[1])) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[u][r] = qvalid ? o_acc[u][r] : 0.0f;
+          for (int u = 0; u < 8; ++u) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o_acc[qt][u][r] = qvalid[qt] ? o_acc[qt][u][r] : 0.0f;
+          }
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int u = 0; u < 8; ++u) {
         u32x2 wv;
         float ov[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = o_acc[u][4 * g + e] * inv;
+        for (int e = 0; e < 4; ++e) ov[e] = o_acc[qt][u][e] * inv[qt];
         wv[0] = pack_out<kBf16>(ov[0], ov[1]);
         wv[1] = pack_out<kBf16>(ov[2], ov[3]);
-        // d = 32u + 8g + 4lh .. +3: 16-byte chunk 4u + g, half lh.
-        *(u32x2*)(stage + li * 256 + 16 * ((4 * u + g) ^ (li & 15)) + 8 * lh) = wv;
+        // Row 16qt + c16, d = 16u + 4g4 .. +3: 16-byte chunk 2u + g4/2, half g4 % 2.
+        *(u32x2*)(stage + (16 * qt + c16) * 256 + 16 * ((2 * u + (g4 >> 1)) ^ c16) + 8 * (g4 & 1)) = wv;
       }
     }
     // Only this wave's rows: LDS operations of one wave complete in order, no barrier. O is
@@ -719,15 +799,20 @@ void bsa_fwd_dma_kernel(Args a) {
       __builtin_nontemporal_store(x, (u32x4*)(oblk + (size_t)row * kHd + 8 * c));
     }
   }
-  if (a.lse && lh == 0) {
-    const float lse = (qvalid && l_tot > 0.0f) ? (m_used + log2f(l_tot)) * kLn2 : -INFINITY;
-    a.lse[(size_t)bh * a.T + qrow] = lse;
+  if (a.lse && g4 == 0) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float lse =
+          (qvalid[qt] && l_tot[qt] > 0.0f) ? (m_used[qt] + log2f(l_tot[qt])) * kLn2 : -INFINITY;
+      a.lse[(size_t)bh * a.T + qrow[qt]] = lse;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pipelined kernel (no seq_lens, CSR or analytic rows): the same work items, LDS layout and
-// per-wave rows as bsa_fwd_dma_kernel, but with Q·K^T of key block b_{i+1}, P·V of b_i and one key
+// Pipelined kernel (no seq_lens, CSR or analytic rows): the same work items and per-wave rows as
+// bsa_fwd_dma_kernel (its own LDS swizzle, V: chunk ^ 4 * (row % 4), and 32x32x16 MFMA layouts
+// with one query row per lane), but with Q·K^T of key block b_{i+1}, P·V of b_i and one key
 // tile's softmax interleaved instruction by instruction, K and V streamed through LDS in 8 KiB
 // sub-tiles. The work item after its coordinates is one generated asm statement
 // (gen_bsa_pipe.py -> bsa_pipe_asm.inc), whose header describes the schedule.
