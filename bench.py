@@ -62,9 +62,10 @@ METRIC = "geomean fwd ms @B2 H16 T8192 D128 over 3 sparsity families; % fp16 MFM
 PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA, published
 PEAK_SCLK_MHZ = 2400  # the shader clock the published peak is quoted at
 FLOP_PER_BLOCK = 4 * 128 ** 3
-# MFMAs the kernel issues for a diagonal block: 160 of a full block's 256 (each wave skips the
-# key tiles above its 32 query rows in Q·K^T and the k-steps above them in P·V).
-DIAG_MFMA_SHARE = 160 / 256
+# v_mfma_f32_16x16x32 the kernel issues for a diagonal block: 304 of a full block's 512 (each wave
+# skips the 16-key tiles above each of its two 16-row query tiles in Q·K^T and the 32-key steps
+# above its rows in P·V).
+DIAG_MFMA_SHARE = 304 / 512
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "bsa_fwd_hbm_traffic_b2h16t8192.txt")
 REF_SEQ_LENS = [8192, 5000]  # variable sequence lengths for the reference-condition lines
 
@@ -106,7 +107,7 @@ def read_traffic():
 
 
 def executed_flop(row_ptr) -> int:
-    """FLOP of the MFMAs the kernel issues: full blocks, and 160/256 of one per diagonal."""
+    """FLOP of the MFMAs the kernel issues: full blocks, and 304/512 of one per diagonal."""
     n_diag = int(np.prod(row_ptr.shape[:-1])) * (row_ptr.shape[-1] - 1)
     return int((P.active_blocks(row_ptr) - n_diag * (1 - DIAG_MFMA_SHARE)) * FLOP_PER_BLOCK)
 
