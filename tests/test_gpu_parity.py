@@ -524,7 +524,7 @@ def _random_case(seed):
     return B, H, T, density, dtype, seq_lens
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(40))
 def test_randomised_shapes_patterns_and_dtypes(seed):
     """Seeded random B, H (B*H not a multiple of 8 takes the row-major work order), T, CSR
     density, seq_lens and dtype against the dense oracle."""
